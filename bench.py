@@ -1,0 +1,288 @@
+"""Benchmark of the grafted-SwiGLU layer path on one MI355X.
+
+Workload (one step): the Llama-3-8B-shape grafted MLP layer with bf16
+weights/activations and fp32 accumulation -- hidden 4096, base intermediate
+14336, one appended graft slice of 1024 neurons, 8 x 2048 = 16384 tokens --
+    RMSNorm fwd (eps 1e-5) -> grafted MLP fwd -> graft-only MLP bwd (dX and
+    per-slice dW) -> RMSNorm bwd -> AdamW on the graft params (lr 1e-4,
+    betas 0.9/0.999, wd 0.01, no clip).
+Inputs are synthetic (weights ~N(0,0.02), x ~N(0,1), gamma ~1+N(0,0.02),
+dy ~N(0,1)), drawn on the GPU and resident in HBM before timing.
+
+Also measured: shadow_bake materialising 32 layers of baked [15360,4096] /
+[4096,15360] matrices (GB/s against HBM), and the oracle (C restatement of
+the reference path) on a bounded token sample on the host cores.
+
+Prints ONE JSON line. Usage: python bench.py [--steps K] [--warmup W]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "graft MLP fwd+bwd tokens/sec @Llama-3-8B shape; % bf16 MFMA peak; bake GB/s"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E (published)
+
+M, D, I, S = 16384, 4096, 14336, 1024
+N = I + S
+EPS = 1e-5
+LR, B1, B2, AEPS, WD = 1e-4, 0.9, 0.999, 1e-8, 0.01
+
+# algorithmic work per launch (FLOP) of each GEMM kernel of one step
+GEMM_FLOP = {
+    "gate_up": 2 * M * D * 2 * N,   # gate + up over N = I + S neurons
+    "down": 2 * M * N * D,          # K-concat of base and graft columns
+    "dinter": 2 * M * D * N,        # dInter with the SiLU*up derivative epilogue
+    "dx": 2 * M * 2 * N * D,        # concat-K over [dgate | dup]
+    "wgrad": 3 * 2 * S * D * M,     # dW gate/up/down of the slice (one launch)
+}
+STEP_FLOP = sum(GEMM_FLOP.values())
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-bake", action="store_true", help="skip the shadow_bake measurement")
+    ap.add_argument("--cpu-tokens", type=int, default=1536)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from glt_amd import _ffi as F, synth
+
+    lib = F.load()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    bf = torch.bfloat16
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+    def fill(t, seed, tid, mean, std):
+        F.call("glt_fill_normal", p(t), F.DTYPE_BF16 if t.dtype == bf else F.DTYPE_F32, t.numel(), seed, tid,
+               mean, std, sp)
+        return t
+
+    log("[bench] drawing inputs")
+    x_raw = fill(torch.empty((M, D), dtype=bf, device=dev), synth.SEED_X, synth.TID_X, 0.0, 1.0)
+    gamma = fill(torch.empty(D, dtype=bf, device=dev), synth.SEED_GAMMA, synth.TID_GAMMA, 1.0, 0.02)
+    dy = fill(torch.empty((M, D), dtype=bf, device=dev), synth.SEED_DY, synth.TID_DY, 0.0, 1.0)
+    wg = fill(torch.empty((I, D), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_GATE, 0.0, 0.02)
+    wu = fill(torch.empty((I, D), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_UP, 0.0, 0.02)
+    wd = fill(torch.empty((D, I), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_DOWN, 0.0, 0.02)
+    masters = fill(torch.empty(3 * S * D, dtype=torch.float32, device=dev), 1, 1, 0.0, 0.02)
+    packed = torch.empty(6 * S * D, dtype=bf, device=dev)
+    wg_t, wu_t = torch.empty((D, I), dtype=bf, device=dev), torch.empty((D, I), dtype=bf, device=dev)
+    wd_t = torch.empty((I, D), dtype=bf, device=dev)
+
+    sl = (F.GraftSlice * 1)()
+    sl[0] = F.GraftSlice(I, S, 0, D, masters.data_ptr(), masters.data_ptr() + 4 * S * D,
+                         masters.data_ptr() + 8 * S * D, packed.data_ptr())
+    desc = F.MlpDesc(M, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT, 1, sl, None)
+    F.call("glt_base_prepare", ctypes.byref(desc), p(wg), p(wu), p(wd), p(wg_t), p(wu_t), p(wd_t), sp)
+    F.call("glt_graft_pack", sl, p(packed), sp)
+    base = F.BaseWeights(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), wg_t.data_ptr(), wu_t.data_ptr(),
+                         wd_t.data_ptr())
+
+    x = torch.empty((M, D), dtype=bf, device=dev)
+    var = torch.empty(M, dtype=torch.float32, device=dev)
+    y = torch.empty((M, D), dtype=bf, device=dev)
+    g = torch.empty((M, N), dtype=bf, device=dev)
+    u = torch.empty((M, N), dtype=bf, device=dev)
+    inter = torch.empty((M, N), dtype=bf, device=dev)
+    dx = torch.empty((M, D), dtype=torch.float32, device=dev)
+    dx_raw = torch.empty((M, D), dtype=torch.float32, device=dev)
+    grads = torch.zeros(3 * S * D, dtype=torch.float32, device=dev)
+    adam_m = torch.zeros(3 * S * D, dtype=torch.float32, device=dev)
+    adam_v = torch.zeros(3 * S * D, dtype=torch.float32, device=dev)
+    gg = (F.GraftGrads * 1)()
+    gg[0] = F.GraftGrads(grads.data_ptr(), grads.data_ptr() + 4 * S * D, grads.data_ptr() + 8 * S * D)
+    ws_bytes = lib.glt_mlp_bwd_workspace_size(ctypes.byref(desc))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    gptr = F.ptr_array([grads.data_ptr()])
+    mptr, vptr = F.ptr_array([adam_m.data_ptr()]), F.ptr_array([adam_v.data_ptr()])
+    pkptr = F.ptr_array([packed.data_ptr()])
+
+    def step(i):
+        F.call("glt_rmsnorm_fwd", p(x_raw), p(gamma), p(x), p(var), M, D, EPS, sp)
+        F.call("glt_mlp_fwd", ctypes.byref(desc), ctypes.byref(base), p(x), p(y), p(g), p(u), p(inter), sp)
+        F.call("glt_mlp_bwd", ctypes.byref(desc), ctypes.byref(base), p(x), p(dy), p(g), p(u), p(inter), p(dx), gg,
+               p(ws), ws_bytes, sp)
+        F.call("glt_rmsnorm_bwd", p(dx), p(x_raw), p(gamma), p(var), p(dx_raw), M, D, EPS, sp)
+        F.call("glt_adamw_graft_step", sl, 1, gptr, mptr, vptr, pkptr, 7, i, LR, B1, B2, AEPS, WD, sp)
+
+    log("[bench] warmup")
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # timed region: K steps between events on the launch stream
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    log(f"[bench] {ms_step:.3f} ms/step")
+
+    # per-kernel durations: the same steps again with launch timing on
+    F.call("glt_profile_enable", 1)
+    for i in range(args.steps):
+        step(args.warmup + args.steps + i)
+    torch.cuda.synchronize()
+    prof = F.profile_collect()
+    F.call("glt_profile_enable", 0)
+    kernels = {k: {"avg_ms": tot / cnt, "launches_per_step": cnt / args.steps} for k, (tot, cnt) in prof.items()}
+    for k, v in kernels.items():
+        v["ms_per_step"] = v["avg_ms"] * v["launches_per_step"]
+        if k in GEMM_FLOP:  # per-step FLOP over per-step time of that kernel
+            v["tflops"] = GEMM_FLOP[k] / (v["ms_per_step"] * 1e-3) / 1e12
+            v["mfma_frac"] = v["tflops"] / PEAK_BF16_TFLOPS
+    gemm_ms = sum(kernels[k]["ms_per_step"] for k in GEMM_FLOP if k in kernels)
+    dom = max((k for k in kernels if k in GEMM_FLOP), key=lambda k: kernels[k]["ms_per_step"])
+    dom_flop = GEMM_FLOP[dom] / kernels[dom]["launches_per_step"]  # per launch
+    achieved = dom_flop / (kernels[dom]["avg_ms"] * 1e-3) / 1e12
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"traffic_{dom}.json")
+    if os.path.exists(tf):
+        traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "flop_per_launch": dom_flop}
+
+    # shadow_bake: 32 layers materialised (config 4)
+    bake = None
+    if not args.no_bake:
+        bake = bench_bake(torch, F, lib, dev, sp, p)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, args.cpu_tokens, wg, wu, wd, masters, x_raw, gamma, dy)
+
+    out = {
+        "metric": METRIC,
+        "value": round(M / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "Llama-3-8B-shape grafted SwiGLU MLP layer: RMSNorm + graft-only fwd+bwd + AdamW",
+                   "tokens": M, "hidden": D, "base_intermediate": I, "graft_slice": S, "parallelism": "none (1 GPU)"},
+        "step_mfma_frac": round(STEP_FLOP / (ms_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "gemm_mfma_frac": round(STEP_FLOP / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "bake": bake,
+        "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in sorted(kernels.items())},
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_bake(torch, F, lib, dev, sp, p, L=32, reps=5):
+    """Config 4: base gate/up [14336,4096] and down [4096,14336] bf16 plus a
+    1024-neuron bf16 graft per layer, materialised into [15360,4096] /
+    [4096,15360] for 32 layers. Algorithmic bytes: read base + read graft +
+    write baked."""
+    bf = torch.bfloat16
+    log("[bench] bake: allocating 32 layers")
+    bases = [[torch.empty(sh, dtype=bf, device=dev) for sh in ((I, D), (I, D), (D, I))] for _ in range(L)]
+    outs = [[torch.empty(sh, dtype=bf, device=dev) for sh in ((N, D), (N, D), (D, N))] for _ in range(L)]
+    grafts = [torch.empty(3 * S * D, dtype=bf, device=dev) for _ in range(L)]
+    for l in range(L):
+        for q, t in enumerate(bases[l]):
+            F.call("glt_fill_normal", p(t), F.DTYPE_BF16, t.numel(), 0, 1000 + 3 * l + q, 0.0, 0.02, sp)
+        F.call("glt_fill_normal", p(grafts[l]), F.DTYPE_BF16, grafts[l].numel(), 1, 2000 + l, 0.0, 0.02, sp)
+    pl = (ctypes.c_int32 * 4)(I, S, 0, D)
+    gp = F.ptr_array([t.data_ptr() for t in grafts])
+    desc = F.BakeDesc(F.BAKE_MATERIALIZE, L, 0, L - 1, 7, D, I, N, F.DTYPE_BF16, 1, pl, gp)
+    arrs = [F.ptr_array([bases[l][q].data_ptr() for l in range(L)]) for q in range(3)]
+    oarrs = [F.ptr_array([outs[l][q].data_ptr() for l in range(L)]) for q in range(3)]
+
+    def run():
+        st = F.ModelState(0)
+        F.call("glt_shadow_bake", ctypes.byref(desc), ctypes.byref(st), arrs[0], arrs[1], arrs[2], oarrs[0],
+               oarrs[1], oarrs[2], sp)
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    F.call("glt_profile_enable", 1)
+    run()
+    torch.cuda.synchronize()
+    prof = F.profile_collect()
+    F.call("glt_profile_enable", 0)
+    nbytes = L * 3 * 2 * (I * D + S * D + N * D)
+    kern_ms = prof.get("bake", (ms, 1))[0]
+    del bases, outs, grafts
+    torch.cuda.empty_cache()
+    return {"layers": L, "bytes": nbytes, "ms": round(ms, 4), "GB_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "kernel_ms": round(kern_ms, 4), "launches": prof.get("bake", (0, 0))[1]}
+
+
+def cpu_baseline(torch, T, wg, wu, wd, masters, x_raw, gamma, dy):
+    """The oracle (C restatement of the reference path, f64 accumulation,
+    OpenMP) on the first T tokens of the same step: RMSNorm fwd, grafted MLP
+    fwd, graft-only bwd, RMSNorm bwd, AdamW."""
+    import numpy as np
+    from oracle import oracle as O
+    log(f"[bench] cpu baseline on {T} tokens")
+    h = lambda t: t.float().cpu().numpy()
+    Wg, Wu, Wd = h(wg), h(wu), h(wd)
+    ms = h(masters).reshape(3, S, D)
+    xr, gm, dyy = h(x_raw[:T]), h(gamma), h(dy[:T])
+    sl = [{"i0": I, "s": S, "h0": 0, "h": D, "gate": ms[0], "up": ms[1], "down": ms[2]}]
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    xn, var = O.rmsnorm_fwd(xr, gm, EPS)
+    g, u, inter, y = O.mlp_fwd(xn, Wg, Wu, Wd, N, sl)
+    dxn, grads = O.mlp_bwd(xn, Wg, Wu, Wd, N, sl, g, u, inter, dyy)
+    O.rmsnorm_bwd(dxn, xr, gm, var, EPS)
+    for q in range(3):
+        O.adamw(ms[q], grads[0][q], np.zeros_like(ms[q]), np.zeros_like(ms[q]), 0, LR, B1, B2, AEPS, WD)
+    dt = time.perf_counter() - t0
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(T / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{T} of the {M} tokens of one step (RMSNorm, grafted MLP fwd, graft-only bwd, RMSNorm bwd, "
+                      f"AdamW), {dt:.2f} s; C oracle with f64 accumulation, {threads} OpenMP threads on {cpu_model}"}
+
+
+if __name__ == "__main__":
+    main()

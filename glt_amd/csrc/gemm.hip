@@ -1,0 +1,524 @@
+// Segment-list GEMM kernels: the gfx950 bf16 MFMA kernel and the strided
+// generic kernel (f32 path, unaligned shapes, graft-GEMM probes).
+#include <cmath>
+
+#include "gemm.hpp"
+
+namespace glt {
+
+// ---------------------------------------------------------------- epilogue
+template <typename TO>
+__device__ __forceinline__ float ld_elem(const void* p, int64_t i) {
+  if constexpr (sizeof(TO) == 4) return static_cast<const float*>(p)[i];
+  else return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <typename TO>
+__device__ __forceinline__ void st_elem(void* p, int64_t i, float v) {
+  if constexpr (sizeof(TO) == 4) static_cast<float*>(p)[i] = v;
+  else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+template <typename TO>
+__device__ __forceinline__ float round_like(float v) {
+  if constexpr (sizeof(TO) == 4) return v;
+  else return bf16_to_f32(f32_to_bf16(v));
+}
+
+// a0 = accumulator (gate accumulator in the dual form), a1 = up accumulator.
+template <typename TO, int MODE>
+__device__ __forceinline__ void epilogue(const GProb& P, int m, int n, float a0, float a1) {
+  if (m >= P.M || n >= P.N) return;
+  const int64_t o = (int64_t)m * P.ldo + n;
+  if constexpr (MODE == EPI_STORE) {
+    float v = P.alpha * a0;
+    if (P.beta != 0.f) v += P.beta * ld_elem<TO>(P.out0, o);
+    st_elem<TO>(P.out0, o, v);
+  } else if constexpr (MODE == EPI_SILU) {
+    // gate/up pre-activations leave the accumulator rounded to the path
+    // dtype (bf16 in the reference, src/layer_forward_impl.inc:72,122), and
+    // silu(g)*u is formed from those values with the reference's f32 order
+    // (src/kernels_elementwise_impl.inc:440-446): sg = 1/(1+exp(-g)), (g*sg)*u.
+    const float g = round_like<TO>(a0), u = round_like<TO>(a1);
+    const float sg = 1.0f / (1.0f + expf(-g));
+    st_elem<TO>(P.out0, o, g * sg * u);
+    if (P.out1) st_elem<TO>(P.out1, o, g);
+    if (P.out2) st_elem<TO>(P.out2, o, u);
+  } else {
+    // SiLU*up derivative on the dInter accumulator
+    // (reference fused_gate_up_bwd_kernel, src/kernels_elementwise_impl.inc:107-117).
+    const int64_t oa = (int64_t)m * P.ldaux + n;
+    const float g = ld_elem<TO>(P.aux0, oa), u = ld_elem<TO>(P.aux1, oa);
+    const float sg = 1.0f / (1.0f + expf(-g));
+    const float gv = g * sg;
+    const float sgrad = sg * (1.0f + g * (1.0f - sg));
+    st_elem<TO>(P.out0, o, a0 * u * sgrad);
+    st_elem<TO>(P.out1, o, a0 * gv);
+  }
+}
+
+// Locates this workgroup's problem and tile. XCD-aware: consecutive
+// workgroup ids are dealt round-robin over the 8 XCDs, so ids are remapped
+// to give each XCD one contiguous range of tiles; within a problem tiles run
+// in groups of kGroupM M-tiles so neighbouring workgroups share A and B rows
+// in that XCD's L2.
+constexpr int kGroupM = 8;
+__device__ __forceinline__ int locate_tile(const GArgs& args, int& tm, int& tn, bool xcd_remap) {
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if (xcd_remap && (nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  int pi = 0;
+  while (pi + 1 < args.nprob && bid >= args.p[pi + 1].tile_begin) ++pi;
+  const GProb& P = args.p[pi];
+  const int t = bid - P.tile_begin;
+  const int per_group = kGroupM * P.tiles_n;
+  const int g = t / per_group;
+  const int first_m = g * kGroupM;
+  const int gm = min(P.tiles_m - first_m, kGroupM);
+  const int r = t - g * per_group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+  return pi;
+}
+
+__device__ __forceinline__ bool seg_hits(const GSeg& S, const GProb& P, int n0, int bn) {
+  return S.K > 0 && max(S.n_lo, n0) < min(min(S.n_hi, P.N), n0 + bn);
+}
+
+// =========================================================================
+// gfx950 MFMA kernel: bf16 x bf16 -> f32, v_mfma_f32_32x32x16_bf16.
+//
+// Workgroup tile 256 (M) x 256 B-rows x 64 (K), 4 wavefronts in a 2x2
+// arrangement; each wavefront owns 128x128 outputs = 4x4 MFMA 32x32 tiles
+// (256 fp32 accumulators per lane). Plain form: the 256 B-rows are 256
+// output columns. Dual form: B-rows [0,128) are gate rows and [128,256) the
+// up rows of the same 128 output columns.
+//
+// Global -> LDS: 16-byte raw buffer loads (out-of-range rows read as zero),
+// staged through registers one K-step ahead, LDS double buffered (2 x 64 KB).
+// LDS rows are 128 bytes; the 16-byte chunk index is XOR-swizzled with the
+// row so both the row-wise stores and the MFMA fragment reads (32 rows x
+// one chunk) spread over all banks.
+// =========================================================================
+constexpr int kBM = 256, kBK = 64;
+constexpr int kTileElems = kBM * kBK;              // one operand tile
+constexpr size_t kMfmaLds = 2 * 2 * kTileElems * 2;  // 2 buffers x (A,B) x bf16
+
+__device__ __forceinline__ int swz(int row, int kc) { return row * kBK + ((kc ^ (row & 7)) << 3); }
+
+constexpr int kEpPitch = 132;  // f32 words per staged epilogue row (128 + pad)
+
+__device__ __forceinline__ void unpack8(const u32x4& q, float* f) {
+  f[0] = bf16_to_f32((uint16_t)(q.x & 0xFFFF)); f[1] = bf16_to_f32((uint16_t)(q.x >> 16));
+  f[2] = bf16_to_f32((uint16_t)(q.y & 0xFFFF)); f[3] = bf16_to_f32((uint16_t)(q.y >> 16));
+  f[4] = bf16_to_f32((uint16_t)(q.z & 0xFFFF)); f[5] = bf16_to_f32((uint16_t)(q.z >> 16));
+  f[6] = bf16_to_f32((uint16_t)(q.w & 0xFFFF)); f[7] = bf16_to_f32((uint16_t)(q.w >> 16));
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 q;
+  q.x = pack_bf16x2(f[0], f[1]); q.y = pack_bf16x2(f[2], f[3]);
+  q.z = pack_bf16x2(f[4], f[5]); q.w = pack_bf16x2(f[6], f[7]);
+  return q;
+}
+template <typename TO>
+__device__ __forceinline__ void ld8(const void* p, int64_t o, float* f) {
+  if constexpr (sizeof(TO) == 4) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + o);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + o + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    unpack8(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p) + o), f);
+  }
+}
+template <typename TO>
+__device__ __forceinline__ void st8(void* p, int64_t o, const float* f) {
+  if constexpr (sizeof(TO) == 4) {
+    float* q = static_cast<float*>(p) + o;
+    *reinterpret_cast<f32x4*>(q) = f32x4{f[0], f[1], f[2], f[3]};
+    *reinterpret_cast<f32x4*>(q + 4) = f32x4{f[4], f[5], f[6], f[7]};
+  } else {
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p) + o) = pack8(f);
+  }
+}
+
+// Eight consecutive output columns n..n+7 of row m (v = accumulators; u =
+// up accumulators in the dual form). Vector path when the chunk is whole;
+// outputs and aux rows are 16-byte aligned (checked on the host).
+template <typename TO, int MODE>
+__device__ __forceinline__ void epi_chunk(const GProb& P, int m, int n, const float* v, const float* u) {
+  if (m >= P.M) return;
+  if (n + 8 > P.N) {
+    for (int j = 0; j < 8; ++j)
+      if (n + j < P.N) epilogue<TO, MODE>(P, m, n + j, v[j], u[j]);
+    return;
+  }
+  const int64_t o = (int64_t)m * P.ldo + n;
+  float r[8];
+  if constexpr (MODE == EPI_STORE) {
+    float old[8];
+    if (P.beta != 0.f) ld8<TO>(P.out0, o, old);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = P.alpha * v[j] + (P.beta != 0.f ? P.beta * old[j] : 0.f);
+    st8<TO>(P.out0, o, r);
+  } else if constexpr (MODE == EPI_SILU) {
+    float g[8], uu[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g[j] = round_like<TO>(v[j]);
+      uu[j] = round_like<TO>(u[j]);
+      const float sg = 1.0f / (1.0f + expf(-g[j]));
+      r[j] = g[j] * sg * uu[j];
+    }
+    st8<TO>(P.out0, o, r);
+    if (P.out1) st8<TO>(P.out1, o, g);
+    if (P.out2) st8<TO>(P.out2, o, uu);
+  } else {
+    float g[8], uu[8], du[8];
+    const int64_t oa = (int64_t)m * P.ldaux + n;
+    ld8<TO>(P.aux0, oa, g);
+    ld8<TO>(P.aux1, oa, uu);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float sg = 1.0f / (1.0f + expf(-g[j]));
+      const float gv = g[j] * sg;
+      const float sgrad = sg * (1.0f + g[j] * (1.0f - sg));
+      r[j] = v[j] * uu[j] * sgrad;
+      du[j] = v[j] * gv;
+    }
+    st8<TO>(P.out0, o, r);
+    st8<TO>(P.out1, o, du);
+  }
+}
+
+template <typename TO, int MODE, bool DUAL>
+__global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  constexpr int BN = DUAL ? 128 : 256;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn;
+  const int pi = locate_tile(args, tm, tn, true);
+  const GProb& P = args.p[pi];
+  const int m0 = tm * kBM, n0 = tn * BN;
+  const int send = P.seg0 + P.nseg;
+
+  auto next_active = [&](int s) {
+    ++s;
+    while (s < send && !seg_hits(args.s[s], P, n0, BN)) ++s;
+    return s;
+  };
+
+  u32x4 ra[8], rb[8];
+  auto gload = [&](int s, int k0) {
+    const GSeg& S = args.s[s];
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(S.A, S.a_bytes);
+    const __amdgpu_buffer_rsrc_t rB0 = make_rsrc(S.B0, S.b0_bytes);
+    const __amdgpu_buffer_rsrc_t rB1 = make_rsrc(DUAL ? S.B1 : S.B0, DUAL ? S.b1_bytes : S.b0_bytes);
+    const int nlo = S.n_lo, nhi = min(S.n_hi, P.N);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      const int m = m0 + row;
+      const uint32_t off =
+          m < P.M ? (uint32_t)(((int64_t)m * S.lda + S.a_col + k0 + kc * 8) * 2) : kOob;
+      ra[i] = buf_load16(rA, off);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      const bool hi = DUAL && i >= 4;  // rows 128..255 of the dual tile
+      const int n = n0 + (DUAL ? (row & 127) : row);
+      const int64_t ld = hi ? S.ldb1 : S.ldb0;
+      const int r0 = hi ? S.b1_row0 : S.b0_row0;
+      const uint32_t off = (n >= nlo && n < nhi) ? (uint32_t)(((int64_t)(n - r0) * ld + k0 + kc * 8) * 2) : kOob;
+      rb[i] = buf_load16(hi ? rB1 : rB0, off);
+    }
+  };
+  auto lstore = [&](int buf) {
+    uint16_t* As = smem + buf * 2 * kTileElems;
+    uint16_t* Bs = As + kTileElems;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      *reinterpret_cast<u32x4*>(As + swz(row, kc)) = ra[i];
+      *reinterpret_cast<u32x4*>(Bs + swz(row, kc)) = rb[i];
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  auto compute = [&](int buf) {
+    const uint16_t* As = smem + buf * 2 * kTileElems;
+    const uint16_t* Bs = As + kTileElems;
+    const int lr = lane & 31, lk = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kc = ks * 2 + lk;
+      bf16x8 a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a[i] = *reinterpret_cast<const bf16x8*>(As + swz(wm * 128 + i * 32 + lr, kc));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int br = DUAL ? ((j >> 1) * 128 + wn * 64 + (j & 1) * 32) : (wn * 128 + j * 32);
+        b[j] = *reinterpret_cast<const bf16x8*>(Bs + swz(br + lr, kc));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  int s = next_active(P.seg0 - 1);
+  if (s < send) {
+    int k0 = 0;
+    gload(s, k0);
+    lstore(0);
+    __syncthreads();
+    int buf = 0;
+    while (true) {
+      int ns = s, nk = k0 + kBK;
+      if (nk >= args.s[s].K) {
+        ns = next_active(s);
+        nk = 0;
+      }
+      const bool more = ns < send;
+      if (more) gload(ns, nk);
+      compute(buf);
+      if (more) lstore(buf ^ 1);
+      __syncthreads();
+      if (!more) break;
+      s = ns;
+      k0 = nk;
+      buf ^= 1;
+    }
+  }
+
+  // Epilogue, staged through LDS (the main loop's last barrier released it):
+  // per 32-row band each wavefront writes its accumulators into a private
+  // 32 x 128 f32 block, then reads it back row-wise so every lane handles 8
+  // consecutive columns with 16-byte loads/stores.
+  // 32x32 accumulator layout: lane holds column (lane & 31), rows
+  // 8*(e/4) + 4*(lane/32) + (e%4) for e = 0..15.
+  float* ep = reinterpret_cast<float*>(smem) + wave * (32 * kEpPitch);
+  const int cr = 4 * (lane >> 5), cc = lane & 31;
+  auto stage = [&](const f32x16* a) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ep[(8 * (e >> 2) + cr + (e & 3)) * kEpPitch + j * 32 + cc] = a[j][e];
+  };
+  // The band loop stays rolled (the chunk code is large); the switch keeps
+  // every accumulator access compile-time indexed, i.e. in registers.
+#pragma unroll 1
+  for (int i = 0; i < 4; ++i) {
+    switch (i) {
+      case 0: stage(acc[0]); break;
+      case 1: stage(acc[1]); break;
+      case 2: stage(acc[2]); break;
+      default: stage(acc[3]); break;
+    }
+    __syncthreads();
+    const int row0 = m0 + wm * 128 + i * 32;
+    if constexpr (DUAL) {
+      // columns [0,64) of the block hold gate, [64,128) up, same output columns
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (lane >> 3) + 8 * q, c8 = (lane & 7) * 8;
+        const float* src = ep + r * kEpPitch + c8;
+        epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 64 + c8, src, src + 64);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int r = (lane >> 4) + 4 * q, c8 = (lane & 15) * 8;
+        const float* src = ep + r * kEpPitch + c8;
+        epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 128 + c8, src, src);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// =========================================================================
+// Generic strided kernel: 64x64 output tile (dual: 64 gate + 64 up columns),
+// K-step 16, operands converted to f32 on load, f32 FMA accumulation.
+// =========================================================================
+template <int KIND>
+__device__ __forceinline__ float ld_kind(const void* p, int64_t i) {
+  if constexpr (KIND == LD_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else if constexpr (KIND == LD_F32) return static_cast<const float*>(p)[i];
+  else return bf16_to_f32(f32_to_bf16(static_cast<const float*>(p)[i]));
+}
+
+template <int LA, int LB, typename TO, int MODE, bool DUAL>
+__global__ void __launch_bounds__(256) gemm_generic_kernel(const GArgs args) {
+  constexpr int BM = 64, BN = 64, BK = 16, NB = DUAL ? 2 : 1;
+  __shared__ float As[BK][BM + 1];
+  __shared__ float Bs[NB][BK][BN + 1];
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  int tm, tn;
+  const int pi = locate_tile(args, tm, tn, false);
+  const GProb& P = args.p[pi];
+  const int m0 = tm * BM, n0 = tn * BN;
+  float acc[NB][4][4] = {};
+  for (int s = P.seg0; s < P.seg0 + P.nseg; ++s) {
+    const GSeg& S = args.s[s];
+    if (!seg_hits(S, P, n0, BN)) continue;
+    const int nhi = min(S.n_hi, P.N);
+    for (int k0 = 0; k0 < S.K; k0 += BK) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = tid + 256 * q, r = e >> 4, kk = e & 15;
+        const int m = m0 + r, k = k0 + kk;
+        As[kk][r] = (m < P.M && k < S.K) ? ld_kind<LA>(S.A, (int64_t)m * S.lda + (int64_t)(S.a_col + k) * S.a_ks) : 0.f;
+#pragma unroll
+        for (int h = 0; h < NB; ++h) {
+          const void* B = h ? S.B1 : S.B0;
+          const int64_t ld = h ? S.ldb1 : S.ldb0;
+          const int r0 = h ? S.b1_row0 : S.b0_row0;
+          const int n = n0 + r;
+          Bs[h][kk][r] = (B && n >= S.n_lo && n < nhi && k < S.K)
+                             ? ld_kind<LB>(B, (int64_t)(n - r0) * ld + (int64_t)k * S.b_ks)
+                             : 0.f;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < BK; ++kk) {
+        float a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = As[kk][tr + 16 * i];
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float b = Bs[h][kk][tc + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[h][i][j] = fmaf(a[i], b, acc[h][i][j]);
+          }
+      }
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      epilogue<TO, MODE>(P, m0 + tr + 16 * i, n0 + tc + 16 * j, acc[0][i][j], DUAL ? acc[NB - 1][i][j] : 0.f);
+}
+
+// ------------------------------------------------------------------ host
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+bool gemm_mfma_eligible(const GemmPlan& plan) {
+  if (plan.a_kind != LD_BF16 || plan.b_kind != LD_BF16) return false;
+  for (int i = 0; i < plan.nseg; ++i) {
+    const GSeg& s = plan.args.s[i];
+    if (s.a_ks != 1 || s.b_ks != 1) return false;
+    if (s.K % kBK != 0 || s.a_col % 8 != 0 || s.lda % 8 != 0 || s.ldb0 % 8 != 0) return false;
+    if (!al16(s.A) || !al16(s.B0)) return false;
+    if (plan.dual && (s.ldb1 % 8 != 0 || !al16(s.B1))) return false;
+  }
+  for (int p = 0; p < plan.args.nprob; ++p) {
+    const GProb& P = plan.args.p[p];
+    // the staged epilogue stores 8-column chunks with 16-byte accesses
+    if (P.ldo % 8 || !al16(P.out0) || !al16(P.out1) || !al16(P.out2)) return false;
+    if (P.mode == EPI_DGDU && (P.ldaux % 8 || !al16(P.aux0) || !al16(P.aux1))) return false;
+    for (int i = P.seg0; i < P.seg0 + P.nseg; ++i) {
+      const GSeg& s = plan.args.s[i];
+      // every byte offset a tile forms must fit the 31-bit buffer range
+      if ((int64_t)(P.M + kBM) * s.lda * 2 >= (int64_t)kOob) return false;
+      if ((int64_t)(s.n_hi - s.b0_row0 + 256) * s.ldb0 * 2 >= (int64_t)kOob) return false;
+      if (plan.dual && (int64_t)(s.n_hi - s.b1_row0 + 256) * s.ldb1 * 2 >= (int64_t)kOob) return false;
+    }
+  }
+  return true;
+}
+
+template <typename TO, int MODE, bool DUAL>
+static glt_status launch_mfma(const GArgs& a, hipStream_t st, const char* label) {
+  static bool attr_set = false;
+  auto fn = gemm_mfma_kernel<TO, MODE, DUAL>;
+  if (!attr_set) {
+    GLT_TRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLds));
+    attr_set = true;
+  }
+  GLT_LAUNCH(label, fn, dim3(a.total_tiles), dim3(256), kMfmaLds, st, a);
+  GLT_LAUNCH_CHECK("gemm_mfma");
+  return GLT_OK;
+}
+
+template <int LA, int LB, typename TO, int MODE, bool DUAL>
+static glt_status launch_generic(const GArgs& a, hipStream_t st, const char* label) {
+  GLT_LAUNCH(label, (gemm_generic_kernel<LA, LB, TO, MODE, DUAL>), dim3(a.total_tiles), dim3(256), 0, st, a);
+  GLT_LAUNCH_CHECK("gemm_generic");
+  return GLT_OK;
+}
+
+glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma) {
+  GArgs& a = plan.args;
+  if (a.nprob == 0) return GLT_OK;
+  const bool mfma = allow_mfma && gemm_mfma_eligible(plan);
+  const int bm = mfma ? kBM : 64;
+  const int bn = mfma ? (plan.dual ? 128 : 256) : 64;
+  const int mode = a.p[0].mode;
+  const int of32 = a.p[0].out_f32;
+  int tiles = 0;
+  for (int p = 0; p < a.nprob; ++p) {
+    GProb& P = a.p[p];
+    GLT_CHECK(P.mode == mode && P.out_f32 == of32, GLT_ERR_INVALID_ARG, "run_gemm: mixed epilogues in one launch");
+    P.tiles_m = (int)cdiv(P.M, bm);
+    P.tiles_n = (int)cdiv(P.N, bn);
+    P.tile_begin = tiles;
+    tiles += P.tiles_m * P.tiles_n;
+  }
+  a.total_tiles = tiles;
+  if (tiles == 0) return GLT_OK;
+  // Rows outside a tile's valid range are steered to kOob explicitly and
+  // every in-range offset fits 31 bits (checked above), so the extent only
+  // has to exclude kOob; a missing operand gets extent 0 and reads as zero.
+  for (int i = 0; i < plan.nseg; ++i) {
+    GSeg& s = a.s[i];
+    s.a_bytes = s.A ? 0x7FFFFFF0u : 0;
+    s.b0_bytes = s.B0 ? 0x7FFFFFF0u : 0;
+    s.b1_bytes = s.B1 ? 0x7FFFFFF0u : 0;
+  }
+  if (mfma) {
+    if (mode == EPI_SILU && plan.dual) return launch_mfma<uint16_t, EPI_SILU, true>(a, st, plan.label);
+    if (mode == EPI_DGDU && !plan.dual) return launch_mfma<uint16_t, EPI_DGDU, false>(a, st, plan.label);
+    if (mode == EPI_STORE && !plan.dual)
+      return of32 ? launch_mfma<float, EPI_STORE, false>(a, st, plan.label)
+                  : launch_mfma<uint16_t, EPI_STORE, false>(a, st, plan.label);
+    set_error("run_gemm: no MFMA kernel for mode %d dual %d", mode, (int)plan.dual);
+    return GLT_ERR_UNSUPPORTED;
+  }
+  const int la = plan.a_kind, lb = plan.b_kind;
+#define GLT_GEN(LA_, LB_, TO_, MODE_, DUAL_)                                                     \
+  if (la == LA_ && lb == LB_ && (sizeof(TO_) == 4) == (of32 != 0) && mode == MODE_ && plan.dual == DUAL_) \
+    return launch_generic<LA_, LB_, TO_, MODE_, DUAL_>(a, st, plan.label);
+  // f32 path
+  GLT_GEN(LD_F32, LD_F32, float, EPI_STORE, false)
+  GLT_GEN(LD_F32, LD_F32, float, EPI_SILU, true)
+  GLT_GEN(LD_F32, LD_F32, float, EPI_DGDU, false)
+  // bf16 path on shapes the MFMA kernel does not take
+  GLT_GEN(LD_BF16, LD_BF16, uint16_t, EPI_STORE, false)
+  GLT_GEN(LD_BF16, LD_BF16, float, EPI_STORE, false)
+  GLT_GEN(LD_BF16, LD_BF16, uint16_t, EPI_SILU, true)
+  GLT_GEN(LD_BF16, LD_BF16, uint16_t, EPI_DGDU, false)
+  // graft-GEMM probes (f32 operands rounded to bf16 on load)
+  GLT_GEN(LD_BF16, LD_F32_AS_BF16, float, EPI_STORE, false)
+  GLT_GEN(LD_F32_AS_BF16, LD_BF16, float, EPI_STORE, false)
+  GLT_GEN(LD_F32_AS_BF16, LD_F32_AS_BF16, float, EPI_STORE, false)
+#undef GLT_GEN
+  set_error("run_gemm: no generic kernel for kinds (%d,%d) out_f32 %d mode %d dual %d", la, lb, of32, mode,
+            (int)plan.dual);
+  return GLT_ERR_UNSUPPORTED;
+}
+
+}  // namespace glt

@@ -1,0 +1,263 @@
+// Library info, error text, conversions, synthetic inputs, transposes,
+// graft mirror packing and the unfused elementwise probes.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "common.hpp"
+
+namespace glt {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+glt_status hip_fail(hipError_t e, const char* what) {
+  set_error("%s failed: %s", what, hipGetErrorString(e));
+  return GLT_ERR_HIP;
+}
+
+// ------------------------------------------------------------ f32 -> bf16
+__global__ void __launch_bounds__(256) f32_to_bf16_kernel(const float* __restrict__ in,
+                                                          uint16_t* __restrict__ out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
+  for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n; i += stride) {
+    if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(in + i) | reinterpret_cast<uintptr_t>(out + i)) & 7) == 0 &&
+        (reinterpret_cast<uintptr_t>(in + i) & 15) == 0) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(in + i);
+      u32x2 o;
+      o.x = pack_bf16x2(v.x, v.y);
+      o.y = pack_bf16x2(v.z, v.w);
+      *reinterpret_cast<u32x2*>(out + i) = o;
+    } else {
+      for (int64_t j = i; j < n && j < i + 4; ++j) out[j] = f32_to_bf16(in[j]);
+    }
+  }
+}
+
+static int grid_for(int64_t work_items, int per_block = 256) {
+  int64_t b = cdiv(work_items, per_block);
+  if (b < 1) b = 1;
+  if (b > 65536) b = 65536;
+  return static_cast<int>(b);
+}
+
+// -------------------------------------------------------- normal generator
+// Counter-based: value i of tensor (seed, tensor_id) depends only on i.
+__host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ void __launch_bounds__(256) fill_normal_kernel(void* out, int dtype, int64_t n,
+                                                          uint64_t key, double mean, double stdev) {
+  const int64_t npairs = (n + 1) / 2;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < npairs; p += stride) {
+    const uint64_t r1 = splitmix64(key + 2 * (uint64_t)p);
+    const uint64_t r2 = splitmix64(key + 2 * (uint64_t)p + 1);
+    const double u1 = (double)((r1 >> 11) + 1) * 0x1.0p-53;  // (0, 1]
+    const double u2 = (double)(r2 >> 11) * 0x1.0p-53;        // [0, 1)
+    const double rad = sqrt(-2.0 * log(u1));
+    const double th = 6.283185307179586 * u2;
+    const float z0 = (float)(mean + stdev * (rad * cos(th)));
+    const float z1 = (float)(mean + stdev * (rad * sin(th)));
+    const int64_t i = 2 * p;
+    if (dtype == GLT_DTYPE_F32) {
+      float* o = static_cast<float*>(out);
+      o[i] = z0;
+      if (i + 1 < n) o[i + 1] = z1;
+    } else {
+      uint16_t* o = static_cast<uint16_t*>(out);
+      o[i] = f32_to_bf16(z0);
+      if (i + 1 < n) o[i + 1] = f32_to_bf16(z1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- transpose
+// dst[c, r] = convert(src[r, c]) for a rows x cols source, through a 64x64
+// LDS tile (f32 staging, padded row to avoid bank conflicts).
+template <typename Tin, typename Tout>
+__device__ __forceinline__ Tout cvt(Tin v);
+template <> __device__ __forceinline__ float cvt<float, float>(float v) { return v; }
+template <> __device__ __forceinline__ uint16_t cvt<uint16_t, uint16_t>(uint16_t v) { return v; }
+template <> __device__ __forceinline__ uint16_t cvt<float, uint16_t>(float v) { return f32_to_bf16(v); }
+
+template <typename Tin, typename Tout>
+__global__ void __launch_bounds__(256) transpose_kernel(const Tin* __restrict__ src,
+                                                        Tout* __restrict__ dst, int rows,
+                                                        int cols, int64_t src_ld) {
+  __shared__ Tin tile[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = r0 + ty + 4 * i, c = c0 + tx;
+    if (r < rows && c < cols) tile[ty + 4 * i][tx] = src[(int64_t)r * src_ld + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = c0 + ty + 4 * i, r = r0 + tx;  // output row c, output col r
+    if (c < cols && r < rows) dst[(int64_t)c * rows + r] = cvt<Tin, Tout>(tile[tx][ty + 4 * i]);
+  }
+}
+
+template <typename Tin, typename Tout>
+static glt_status launch_transpose(const Tin* src, Tout* dst, int rows, int cols, int64_t src_ld,
+                                   hipStream_t st) {
+  if (rows == 0 || cols == 0) return GLT_OK;
+  dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64));
+  GLT_LAUNCH("transpose", (transpose_kernel<Tin, Tout>), grid, dim3(256), 0, st, src, dst, rows, cols, src_ld);
+  GLT_LAUNCH_CHECK("transpose");
+  return GLT_OK;
+}
+
+// dst [cols, rows] (contiguous) = transpose of a rows x cols block whose rows
+// are src_ld elements apart.
+glt_status transpose_any(const void* src, void* dst, int rows, int cols, int64_t src_ld, int dtype,
+                         hipStream_t st) {
+  if (dtype == GLT_DTYPE_F32)
+    return launch_transpose(static_cast<const float*>(src), static_cast<float*>(dst), rows, cols, src_ld, st);
+  return launch_transpose(static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), rows, cols, src_ld,
+                          st);
+}
+
+glt_status transpose_f32_to_bf16(const float* src, uint16_t* dst, int rows, int cols, hipStream_t st) {
+  return launch_transpose(src, dst, rows, cols, (int64_t)cols, st);
+}
+
+glt_status convert_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st) {
+  if (n == 0) return GLT_OK;
+  GLT_LAUNCH("f32_to_bf16", f32_to_bf16_kernel, dim3(grid_for(cdiv(n, 4))), dim3(256), 0, st, in, out, n);
+  GLT_LAUNCH_CHECK("f32_to_bf16");
+  return GLT_OK;
+}
+
+// ------------------------------------------------------ elementwise probes
+// silu(g)*u with the reference's f32 operation order
+// (reference src/kernels_elementwise_impl.inc:395-401): sg = 1/(1+exp(-g)),
+// out = bf16((g*sg)*u).
+__global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* __restrict__ g,
+                                                       const uint16_t* __restrict__ u,
+                                                       uint16_t* __restrict__ out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gp = bf16_to_f32(g[i]);
+    const float uv = bf16_to_f32(u[i]);
+    const float sg = 1.0f / (1.0f + expf(-gp));
+    out[i] = f32_to_bf16(gp * sg * uv);
+  }
+}
+
+// (reference src/kernels_elementwise_impl.inc:107-117)
+__global__ void __launch_bounds__(256) gate_up_bwd_kernel(const float* __restrict__ gi,
+                                                          const uint16_t* __restrict__ g,
+                                                          const uint16_t* __restrict__ u,
+                                                          float* __restrict__ dg,
+                                                          float* __restrict__ du, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gp = bf16_to_f32(g[i]);
+    const float uv = bf16_to_f32(u[i]);
+    const float sg = 1.0f / (1.0f + expf(-gp));
+    const float gv = gp * sg;
+    const float silu_grad = sg * (1.0f + gp * (1.0f - sg));
+    const float giv = gi[i];
+    dg[i] = giv * uv * silu_grad;
+    du[i] = giv * gv;
+  }
+}
+
+}  // namespace glt
+
+using namespace glt;
+
+extern "C" {
+
+int32_t glt_version(void) { return GLT_ABI_VERSION; }
+
+const char* glt_last_error_string(void) { return g_err; }
+
+glt_status glt_device_info(int32_t device, int32_t* cu_count, int32_t* clock_mhz, int64_t* hbm_bytes) {
+  hipDeviceProp_t p;
+  GLT_TRY_HIP(hipGetDeviceProperties(&p, device));
+  if (cu_count) *cu_count = p.multiProcessorCount;
+  if (clock_mhz) *clock_mhz = p.clockRate / 1000;
+  if (hbm_bytes) *hbm_bytes = (int64_t)p.totalGlobalMem;
+  return GLT_OK;
+}
+
+glt_status glt_f32_to_bf16(const float* in, uint16_t* out, int64_t n, void* stream) {
+  GLT_CHECK(n >= 0, GLT_ERR_SHAPE, "glt_f32_to_bf16: n < 0");
+  GLT_CHECK(n == 0 || (in && out), GLT_ERR_INVALID_ARG, "glt_f32_to_bf16: null pointer");
+  return convert_f32_to_bf16(in, out, n, as_stream(stream));
+}
+
+glt_status glt_fill_normal(void* out, int32_t dtype, int64_t n, uint64_t seed, uint64_t tensor_id,
+                           double mean, double stdev, void* stream) {
+  GLT_CHECK(n >= 0, GLT_ERR_SHAPE, "glt_fill_normal: n < 0");
+  GLT_CHECK(n == 0 || out, GLT_ERR_INVALID_ARG, "glt_fill_normal: null pointer");
+  GLT_CHECK(dtype == GLT_DTYPE_F32 || dtype == GLT_DTYPE_BF16, GLT_ERR_DTYPE, "glt_fill_normal: dtype");
+  if (n == 0) return GLT_OK;
+  const uint64_t key = splitmix64(seed ^ splitmix64(tensor_id + 0x632BE59BD9B4E019ull));
+  GLT_LAUNCH("fill_normal", fill_normal_kernel, dim3(grid_for(cdiv(n, 2))), dim3(256), 0, as_stream(stream),
+                     out, dtype, n, key, mean, stdev);
+  GLT_LAUNCH_CHECK("fill_normal");
+  return GLT_OK;
+}
+
+glt_status glt_transpose(const void* src, void* dst, int32_t rows, int32_t cols, int32_t dtype,
+                         void* stream) {
+  GLT_CHECK(rows >= 0 && cols >= 0, GLT_ERR_SHAPE, "glt_transpose: negative shape");
+  GLT_CHECK((rows == 0 || cols == 0) || (src && dst), GLT_ERR_INVALID_ARG, "glt_transpose: null pointer");
+  GLT_CHECK(dtype == GLT_DTYPE_F32 || dtype == GLT_DTYPE_BF16, GLT_ERR_DTYPE, "glt_transpose: dtype");
+  return transpose_any(src, dst, rows, cols, cols, dtype, as_stream(stream));
+}
+
+glt_status glt_graft_pack(const glt_graft_slice* sl, uint16_t* packed, void* stream) {
+  GLT_CHECK(sl && packed, GLT_ERR_INVALID_ARG, "glt_graft_pack: null pointer");
+  GLT_CHECK(sl->s > 0 && sl->h > 0, GLT_ERR_SHAPE, "glt_graft_pack: empty slice");
+  const int64_t sh = (int64_t)sl->s * sl->h;
+  const float* masters[3] = {sl->master_gate, sl->master_up, sl->master_down};
+  hipStream_t st = as_stream(stream);
+  for (int p = 0; p < 3; ++p) {
+    if (!masters[p]) continue;
+    uint16_t* base = packed + 2 * p * sh;
+    glt_status s = convert_f32_to_bf16(masters[p], base, sh, st);
+    if (s != GLT_OK) return s;
+    s = transpose_f32_to_bf16(masters[p], base + sh, sl->s, sl->h, st);
+    if (s != GLT_OK) return s;
+  }
+  return GLT_OK;
+}
+
+glt_status glt_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n, void* stream) {
+  GLT_CHECK(n >= 0, GLT_ERR_SHAPE, "glt_silu_mul: n < 0");
+  GLT_CHECK(n == 0 || (g && u && out), GLT_ERR_INVALID_ARG, "glt_silu_mul: null pointer");
+  if (n == 0) return GLT_OK;
+  GLT_LAUNCH("silu_mul", silu_mul_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), g, u, out, n);
+  GLT_LAUNCH_CHECK("silu_mul");
+  return GLT_OK;
+}
+
+glt_status glt_gate_up_bwd(const float* gi, const uint16_t* g, const uint16_t* u, float* dg, float* du,
+                           int64_t n, void* stream) {
+  GLT_CHECK(n >= 0, GLT_ERR_SHAPE, "glt_gate_up_bwd: n < 0");
+  GLT_CHECK(n == 0 || (gi && g && u && dg && du), GLT_ERR_INVALID_ARG, "glt_gate_up_bwd: null pointer");
+  if (n == 0) return GLT_OK;
+  GLT_LAUNCH("gate_up_bwd", gate_up_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), gi, g, u, dg,
+                     du, n);
+  GLT_LAUNCH_CHECK("gate_up_bwd");
+  return GLT_OK;
+}
+
+}  // extern "C"

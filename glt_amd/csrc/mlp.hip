@@ -1,0 +1,420 @@
+// Grafted SwiGLU MLP: forward, graft-only backward, graft-GEMM probes,
+// base preparation. Host code that turns a glt_mlp_desc into segment-list
+// GEMM launches (see gemm.hpp).
+#include <algorithm>
+
+#include "gemm.hpp"
+
+namespace glt {
+
+glt_status transpose_any(const void* src, void* dst, int rows, int cols, int64_t src_ld, int dtype,
+                         hipStream_t st);
+
+static size_t esize(int dtype) { return dtype == GLT_DTYPE_F32 ? 4 : 2; }
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Packed bf16 mirror sub-blocks (glt_graft_slice.packed):
+// gate[S,H], gate^T[H,S], up[S,H], up^T[H,S], down[S,H], down^T[H,S].
+static const uint16_t* packed_block(const glt_graft_slice& s, int proj, bool transposed) {
+  const int64_t sh = (int64_t)s.s * s.h;
+  return s.packed + (2 * proj + (transposed ? 1 : 0)) * sh;
+}
+
+static glt_status check_desc(const glt_mlp_desc* d, const glt_base_weights* w, const char* who) {
+  GLT_CHECK(d && w, GLT_ERR_INVALID_ARG, "%s: null descriptor", who);
+  GLT_CHECK(d->dtype == GLT_DTYPE_BF16 || d->dtype == GLT_DTYPE_F32, GLT_ERR_DTYPE, "%s: dtype %d", who, d->dtype);
+  GLT_CHECK(d->M >= 0 && d->D > 0 && d->I >= 0 && d->N >= d->I && d->N > 0, GLT_ERR_SHAPE,
+            "%s: bad dims M=%d D=%d I=%d N=%d", who, d->M, d->D, d->I, d->N);
+  GLT_CHECK(d->n_slices >= 0 && d->n_slices <= 7, GLT_ERR_UNSUPPORTED, "%s: %d slices (max 7)", who, d->n_slices);
+  GLT_CHECK(d->n_slices == 0 || d->slices, GLT_ERR_INVALID_ARG, "%s: null slices", who);
+  GLT_CHECK(d->I == 0 || (w->gate && w->up && w->down), GLT_ERR_INVALID_ARG, "%s: null base weight", who);
+  const bool explicit_graft = d->flags & GLT_MLP_EXPLICIT;
+  for (int j = 0; explicit_graft && j < d->n_slices; ++j) {
+    const glt_graft_slice& s = d->slices[j];
+    GLT_CHECK(s.i_start >= 0 && s.s > 0 && s.i_start + s.s <= d->N && s.h_start >= 0 && s.h > 0 &&
+                  s.h_start + s.h <= d->D,
+              GLT_ERR_SHAPE, "%s: slice %d {i0=%d S=%d h0=%d H=%d} outside N=%d D=%d", who, j, s.i_start, s.s,
+              s.h_start, s.h, d->N, d->D);
+    const bool any = s.master_gate || s.master_up || s.master_down;
+    GLT_CHECK(d->dtype != GLT_DTYPE_BF16 || !any || s.packed, GLT_ERR_INVALID_ARG,
+              "%s: slice %d has no packed bf16 mirror (glt_graft_pack)", who, j);
+  }
+  return GLT_OK;
+}
+
+static GSeg nt_seg(const void* A, int64_t lda, int a_col, int K, int n_lo, int n_hi, const void* B0, int64_t ldb0,
+                   int b0_row0, const void* B1 = nullptr, int64_t ldb1 = 0, int b1_row0 = 0) {
+  GSeg s{};
+  s.A = A; s.lda = lda; s.a_ks = 1; s.a_col = a_col; s.K = K; s.n_lo = n_lo; s.n_hi = n_hi;
+  s.B0 = B0; s.ldb0 = ldb0; s.b0_row0 = b0_row0; s.B1 = B1; s.ldb1 = ldb1; s.b1_row0 = b1_row0; s.b_ks = 1;
+  return s;
+}
+
+static GProb prob(int M, int N, int mode, bool f32, void* o0, void* o1, void* o2, int64_t ldo,
+                  const void* a0 = nullptr, const void* a1 = nullptr, int64_t ldaux = 0) {
+  GProb p{};
+  p.M = M; p.N = N; p.mode = mode; p.out_f32 = f32; p.alpha = 1.f; p.beta = 0.f;
+  p.out0 = o0; p.out1 = o1; p.out2 = o2; p.ldo = ldo; p.aux0 = a0; p.aux1 = a1; p.ldaux = ldaux;
+  return p;
+}
+
+// gate/up concat-N GEMM with the SiLU*up epilogue.
+static glt_status gate_up_forward(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, void* g_out,
+                                  void* u_out, void* inter, hipStream_t st) {
+  const bool f32 = d->dtype == GLT_DTYPE_F32;
+  GemmPlan plan;
+  plan.dual = true;
+  plan.label = "gate_up";
+  plan.a_kind = plan.b_kind = f32 ? LD_F32 : LD_BF16;
+  plan.add_problem(prob(d->M, d->N, EPI_SILU, f32, inter, g_out, u_out, d->N));
+  if (d->I > 0) plan.add_seg(nt_seg(x, d->D, 0, d->D, 0, d->I, w->gate, d->D, 0, w->up, d->D, 0));
+  if (d->flags & GLT_MLP_EXPLICIT) {
+    for (int j = 0; j < d->n_slices; ++j) {
+      const glt_graft_slice& s = d->slices[j];
+      if (!s.master_gate && !s.master_up) continue;
+      const void* bg = f32 ? (const void*)s.master_gate : (s.master_gate ? packed_block(s, 0, false) : nullptr);
+      const void* bu = f32 ? (const void*)s.master_up : (s.master_up ? packed_block(s, 1, false) : nullptr);
+      plan.add_seg(nt_seg(x, d->D, s.h_start, s.h, s.i_start, s.i_start + s.s, bg, s.h, s.i_start, bu, s.h,
+                          s.i_start));
+    }
+  }
+  return run_gemm(plan, st);
+}
+
+// down projection: K-concat of the base columns and each slice's rows.
+static glt_status down_forward(const glt_mlp_desc* d, const glt_base_weights* w, const void* inter, void* y,
+                               hipStream_t st) {
+  const bool f32 = d->dtype == GLT_DTYPE_F32;
+  GemmPlan plan;
+  plan.label = "down";
+  plan.a_kind = plan.b_kind = f32 ? LD_F32 : LD_BF16;
+  plan.add_problem(prob(d->M, d->D, EPI_STORE, f32, y, nullptr, nullptr, d->D));
+  if (d->I > 0) plan.add_seg(nt_seg(inter, d->N, 0, d->I, 0, d->D, w->down, d->I, 0));
+  if (d->flags & GLT_MLP_EXPLICIT) {
+    for (int j = 0; j < d->n_slices; ++j) {
+      const glt_graft_slice& s = d->slices[j];
+      if (!s.master_down) continue;
+      if (f32) {
+        // B(n = h0+h, k = s) = delta_down[s, h]: read the [S,H] master strided
+        GSeg g = nt_seg(inter, d->N, s.i_start, s.s, s.h_start, s.h_start + s.h, s.master_down, 1, s.h_start);
+        g.b_ks = s.h;
+        plan.add_seg(g);
+      } else {
+        plan.add_seg(nt_seg(inter, d->N, s.i_start, s.s, s.h_start, s.h_start + s.h, packed_block(s, 2, true), s.s,
+                            s.h_start));
+      }
+    }
+  }
+  return run_gemm(plan, st);
+}
+
+struct BwdLayout {
+  size_t dg, du, xt, dyt, g, u, inter, slice0, slice_stride, total;
+  bool mfma;
+};
+
+// MFMA eligibility of the backward's NT GEMMs depends only on alignment,
+// which the workspace layout and these checks settle up front.
+static bool bwd_uses_mfma(const glt_mlp_desc* d) {
+  if (d->dtype != GLT_DTYPE_BF16) return false;
+  if (d->D % 64 || d->I % 64 || d->N % 8 || d->M % 64) return false;
+  if (d->flags & GLT_MLP_EXPLICIT)
+    for (int j = 0; j < d->n_slices; ++j) {
+      const glt_graft_slice& s = d->slices[j];
+      if (s.s % 64 || s.h % 64 || s.i_start % 8 || s.h_start % 8) return false;
+    }
+  return true;
+}
+
+static BwdLayout bwd_layout(const glt_mlp_desc* d) {
+  BwdLayout L{};
+  const size_t es = esize(d->dtype);
+  const size_t MN = (size_t)d->M * d->N * es, MD = (size_t)d->M * d->D * es;
+  L.mfma = bwd_uses_mfma(d);
+  size_t off = 0;
+  L.dg = off; off += align256(MN);
+  L.du = off; off += align256(MN);
+  if (d->flags & GLT_MLP_RECOMPUTE) {
+    L.g = off; off += align256(MN);
+    L.u = off; off += align256(MN);
+    L.inter = off; off += align256(MN);
+  }
+  if (L.mfma) {
+    L.xt = off; off += align256(MD);
+    L.dyt = off; off += align256(MD);
+    L.slice0 = off;
+    size_t per = 0;
+    for (int j = 0; (d->flags & GLT_MLP_EXPLICIT) && j < d->n_slices; ++j)
+      per = std::max(per, 3 * align256((size_t)d->slices[j].s * d->M * es));
+    L.slice_stride = per;
+    off += per * (size_t)((d->flags & GLT_MLP_EXPLICIT) ? d->n_slices : 0);
+  }
+  L.total = off;
+  return L;
+}
+
+}  // namespace glt
+
+using namespace glt;
+
+extern "C" {
+
+glt_status glt_base_prepare(const glt_mlp_desc* d, const void* gate, const void* up, const void* down,
+                            void* gate_t, void* up_t, void* down_t, void* stream) {
+  GLT_CHECK(d && gate && up && down && gate_t && up_t && down_t, GLT_ERR_INVALID_ARG,
+            "glt_base_prepare: null pointer");
+  GLT_CHECK(d->dtype == GLT_DTYPE_BF16 || d->dtype == GLT_DTYPE_F32, GLT_ERR_DTYPE, "glt_base_prepare: dtype");
+  GLT_CHECK(d->D > 0 && d->I >= 0, GLT_ERR_SHAPE, "glt_base_prepare: dims");
+  hipStream_t st = as_stream(stream);
+  glt_status s;
+  if ((s = transpose_any(gate, gate_t, d->I, d->D, d->D, d->dtype, st)) != GLT_OK) return s;
+  if ((s = transpose_any(up, up_t, d->I, d->D, d->D, d->dtype, st)) != GLT_OK) return s;
+  return transpose_any(down, down_t, d->D, d->I, d->I, d->dtype, st);
+}
+
+glt_status glt_mlp_fwd(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, void* y, void* gate_pre,
+                       void* up_pre, void* inter, void* stream) {
+  glt_status s = check_desc(d, w, "glt_mlp_fwd");
+  if (s != GLT_OK) return s;
+  GLT_CHECK(d->M == 0 || (x && y && inter), GLT_ERR_INVALID_ARG, "glt_mlp_fwd: null x/y/inter");
+  if (d->M == 0) return GLT_OK;
+  hipStream_t st = as_stream(stream);
+  if ((s = gate_up_forward(d, w, x, gate_pre, up_pre, inter, st)) != GLT_OK) return s;
+  return down_forward(d, w, inter, y, st);
+}
+
+size_t glt_mlp_bwd_workspace_size(const glt_mlp_desc* d) {
+  if (!d) return 0;
+  return bwd_layout(d).total;
+}
+
+glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, const void* dy,
+                       const void* gate_pre, const void* up_pre, const void* inter, float* dx,
+                       const glt_graft_grads* grads, void* ws, size_t ws_bytes, void* stream) {
+  glt_status s = check_desc(d, w, "glt_mlp_bwd");
+  if (s != GLT_OK) return s;
+  GLT_CHECK(!(d->state && d->state->baked), GLT_ERR_BAKED_NO_BACKWARD,
+            "glt_mlp_bwd: backward on a shadow-baked model is forbidden");
+  const bool recompute = d->flags & GLT_MLP_RECOMPUTE;
+  GLT_CHECK(d->M == 0 || (x && dy && (recompute || (gate_pre && up_pre && inter))), GLT_ERR_INVALID_ARG,
+            "glt_mlp_bwd: null x/dy or saved activations (set GLT_MLP_RECOMPUTE to recompute them)");
+  const bool explicit_graft = d->flags & GLT_MLP_EXPLICIT;
+  GLT_CHECK(!explicit_graft || d->n_slices == 0 || grads, GLT_ERR_INVALID_ARG, "glt_mlp_bwd: null grads");
+  const BwdLayout L = bwd_layout(d);
+  GLT_CHECK(ws_bytes >= L.total && (L.total == 0 || ws), GLT_ERR_WORKSPACE,
+            "glt_mlp_bwd: workspace %zu bytes < required %zu", ws_bytes, L.total);
+  if (d->M == 0) return GLT_OK;
+  GLT_CHECK(d->I == 0 || w->down_t || !L.mfma, GLT_ERR_INVALID_ARG,
+            "glt_mlp_bwd: bf16 path needs the transposed base (glt_base_prepare)");
+  GLT_CHECK(d->I == 0 || !L.mfma || (w->gate_t && w->up_t), GLT_ERR_INVALID_ARG,
+            "glt_mlp_bwd: bf16 path needs the transposed base (glt_base_prepare)");
+  hipStream_t st = as_stream(stream);
+  char* W = static_cast<char*>(ws);
+  const bool f32 = d->dtype == GLT_DTYPE_F32;
+  const int kind = f32 ? LD_F32 : LD_BF16;
+  const int dt = d->dtype;
+  const int M = d->M, D = d->D, I = d->I, N = d->N;
+  void* dg = W + L.dg;
+  void* du = W + L.du;
+
+  if (recompute) {
+    gate_pre = W + L.g;
+    up_pre = W + L.u;
+    inter = W + L.inter;
+    if ((s = gate_up_forward(d, w, x, W + L.g, W + L.u, W + L.inter, st)) != GLT_OK) return s;
+  }
+
+  // 1) dInter = dy . [W_down | grafts] with the SiLU*up derivative epilogue
+  //    (reference src/layer_backward_impl.inc:45-188).
+  {
+    GemmPlan plan;
+    plan.label = "dinter";
+    plan.a_kind = plan.b_kind = kind;
+    plan.add_problem(prob(M, N, EPI_DGDU, f32, dg, du, nullptr, N, gate_pre, up_pre, N));
+    if (I > 0) {
+      if (w->down_t) {
+        plan.add_seg(nt_seg(dy, D, 0, D, 0, I, w->down_t, D, 0));
+      } else {
+        GSeg g = nt_seg(dy, D, 0, D, 0, I, w->down, 1, 0);  // B(n, k) = W_down[k, n]
+        g.b_ks = I;
+        plan.add_seg(g);
+      }
+    }
+    for (int j = 0; explicit_graft && j < d->n_slices; ++j) {
+      const glt_graft_slice& sl = d->slices[j];
+      if (!sl.master_down) continue;
+      // B(n = i0+s, k = h) = delta_down[s, h]: the [S,H] storage is NT as is
+      const void* B = f32 ? (const void*)sl.master_down : packed_block(sl, 2, false);
+      plan.add_seg(nt_seg(dy, D, sl.h_start, sl.h, sl.i_start, sl.i_start + sl.s, B, sl.h, sl.i_start));
+    }
+    if ((s = run_gemm(plan, st)) != GLT_OK) return s;
+  }
+
+  // 2) dX = [dgate | dup] . [W_gate ; W_up (+) grafts]  (f32 out)
+  //    (reference src/layer_backward_impl.inc:307-361).
+  if (dx) {
+    GemmPlan plan;
+    plan.label = "dx";
+    plan.a_kind = plan.b_kind = kind;
+    plan.add_problem(prob(M, D, EPI_STORE, true, dx, nullptr, nullptr, D));
+    if (I > 0) {
+      const void* wt[2] = {w->gate_t, w->up_t};
+      const void* wo[2] = {w->gate, w->up};
+      const void* a[2] = {dg, du};
+      for (int p = 0; p < 2; ++p) {
+        if (wt[p]) {
+          plan.add_seg(nt_seg(a[p], N, 0, I, 0, D, wt[p], I, 0));
+        } else {
+          GSeg g = nt_seg(a[p], N, 0, I, 0, D, wo[p], 1, 0);  // B(n, k) = W[k, n]
+          g.b_ks = D;
+          plan.add_seg(g);
+        }
+      }
+    }
+    for (int j = 0; explicit_graft && j < d->n_slices; ++j) {
+      const glt_graft_slice& sl = d->slices[j];
+      const float* mast[2] = {sl.master_gate, sl.master_up};
+      const void* a[2] = {dg, du};
+      for (int p = 0; p < 2; ++p) {
+        if (!mast[p]) continue;
+        if (f32) {
+          GSeg g = nt_seg(a[p], N, sl.i_start, sl.s, sl.h_start, sl.h_start + sl.h, mast[p], 1, sl.h_start);
+          g.b_ks = sl.h;  // B(n = h0+h, k = s) = delta[s, h]
+          plan.add_seg(g);
+        } else {
+          plan.add_seg(nt_seg(a[p], N, sl.i_start, sl.s, sl.h_start, sl.h_start + sl.h, packed_block(sl, p, true),
+                              sl.s, sl.h_start));
+        }
+      }
+    }
+    if ((s = run_gemm(plan, st)) != GLT_OK) return s;
+  }
+
+  // 3) per-slice weight gradients, reduced over the M tokens, [S,H] storage
+  //    (reference src/graft_ops_impl.inc:120-141, :214-228):
+  //      dGate = dgate_i^T . x_h, dUp = dup_i^T . x_h, dDown = inter_i^T . dy_h
+  if (!explicit_graft || d->n_slices == 0) return GLT_OK;
+  if (L.mfma) {
+    // K (= tokens) must be the contiguous axis of both operands for the MFMA
+    // kernel: transpose x, dy and each slice's column blocks once.
+    char* XT = W + L.xt;
+    char* DYT = W + L.dyt;
+    if ((s = transpose_any(x, XT, M, D, D, dt, st)) != GLT_OK) return s;
+    if ((s = transpose_any(dy, DYT, M, D, D, dt, st)) != GLT_OK) return s;
+    GemmPlan plan;
+    plan.label = "wgrad";
+    plan.a_kind = plan.b_kind = LD_BF16;
+    const size_t es = esize(dt);
+    for (int j = 0; j < d->n_slices; ++j) {
+      const glt_graft_slice& sl = d->slices[j];
+      const glt_graft_grads& gr = grads[j];
+      char* base = W + L.slice0 + (size_t)j * L.slice_stride;
+      const size_t blk = align256((size_t)sl.s * M * es);
+      char* srcs[3] = {static_cast<char*>(dg), static_cast<char*>(du), (char*)inter};
+      float* outs[3] = {gr.gate, gr.up, gr.down};
+      const float* mast[3] = {sl.master_gate, sl.master_up, sl.master_down};
+      for (int p = 0; p < 3; ++p) {
+        if (!outs[p] || !mast[p]) continue;
+        char* AT = base + p * blk;
+        if ((s = transpose_any(srcs[p] + (size_t)sl.i_start * es, AT, M, sl.s, N, dt, st)) != GLT_OK) return s;
+        const char* BT = (p < 2 ? XT : DYT) + (size_t)sl.h_start * M * es;
+        if (plan.args.nprob == kMaxProb) {
+          if ((s = run_gemm(plan, st)) != GLT_OK) return s;
+          plan = GemmPlan();
+          plan.label = "wgrad";
+          plan.a_kind = plan.b_kind = LD_BF16;
+        }
+        plan.add_problem(prob(sl.s, sl.h, EPI_STORE, true, outs[p], nullptr, nullptr, sl.h));
+        plan.add_seg(nt_seg(AT, M, 0, M, 0, sl.h, BT, M, 0));
+      }
+    }
+    return run_gemm(plan, st);
+  }
+  // strided (generic) form: A(s, t) = src[t*N + i0 + s], B(h, t) = src2[t*D + h0 + h]
+  GemmPlan plan;
+  plan.label = "wgrad";
+  plan.a_kind = plan.b_kind = kind;
+  const size_t es = esize(dt);
+  for (int j = 0; j < d->n_slices; ++j) {
+    const glt_graft_slice& sl = d->slices[j];
+    const glt_graft_grads& gr = grads[j];
+    const char* srcs[3] = {static_cast<const char*>(dg), static_cast<const char*>(du),
+                           static_cast<const char*>(inter)};
+    const char* srcb[3] = {static_cast<const char*>(x), static_cast<const char*>(x), static_cast<const char*>(dy)};
+    float* outs[3] = {gr.gate, gr.up, gr.down};
+    const float* mast[3] = {sl.master_gate, sl.master_up, sl.master_down};
+    for (int p = 0; p < 3; ++p) {
+      if (!outs[p] || !mast[p]) continue;
+      if (plan.args.nprob == kMaxProb) {
+        if ((s = run_gemm(plan, st)) != GLT_OK) return s;
+        plan = GemmPlan();
+        plan.label = "wgrad";
+        plan.a_kind = plan.b_kind = kind;
+      }
+      plan.add_problem(prob(sl.s, sl.h, EPI_STORE, true, outs[p], nullptr, nullptr, sl.h));
+      GSeg g = nt_seg(srcs[p] + (size_t)sl.i_start * es, 1, 0, M, 0, sl.h, srcb[p] + (size_t)sl.h_start * es, 1, 0);
+      g.a_ks = N;
+      g.b_ks = D;
+      plan.add_seg(g);
+    }
+  }
+  return run_gemm(plan, st);
+}
+
+glt_status glt_graft_gemm(int32_t kind, int32_t M, int32_t S, int32_t H, const uint16_t* a, int64_t lda,
+                          const float* delta, const float* dy, float* out, int64_t ldo, float alpha, float beta,
+                          void* stream) {
+  GLT_CHECK(M >= 0 && S > 0 && H > 0, GLT_ERR_SHAPE, "glt_graft_gemm: M=%d S=%d H=%d", M, S, H);
+  GLT_CHECK(kind >= GLT_GEMM_EXPAND_FWD && kind <= GLT_GEMM_CONTRACT_IGRAD, GLT_ERR_INVALID_ARG,
+            "glt_graft_gemm: kind %d", kind);
+  GLT_CHECK(out, GLT_ERR_INVALID_ARG, "glt_graft_gemm: null out");
+  const bool needs_a = kind <= GLT_GEMM_CONTRACT_WGRAD;
+  const bool needs_delta = kind == GLT_GEMM_EXPAND_FWD || kind == GLT_GEMM_CONTRACT_FWD || kind >= GLT_GEMM_EXPAND_IGRAD;
+  const bool needs_dy = kind >= GLT_GEMM_EXPAND_WGRAD;
+  GLT_CHECK((!needs_a || a) && (!needs_delta || delta) && (!needs_dy || dy), GLT_ERR_INVALID_ARG,
+            "glt_graft_gemm: missing operand for kind %d", kind);
+  GemmPlan plan;
+  plan.label = "graft_gemm";
+  GSeg g{};
+  g.a_col = 0;
+  g.n_lo = 0;
+  g.b0_row0 = 0;
+  int outM = M, outN = 0;
+  switch (kind) {
+    case GLT_GEMM_EXPAND_FWD:  // out[M,S] = a[M,H] . bf16(delta[S,H])^T
+      plan.a_kind = LD_BF16; plan.b_kind = LD_F32_AS_BF16; outN = S;
+      g.A = a; g.lda = lda; g.a_ks = 1; g.K = H; g.B0 = delta; g.ldb0 = H; g.b_ks = 1;
+      break;
+    case GLT_GEMM_CONTRACT_FWD:  // out[M,H] = a[M,S] . bf16(delta[S,H])
+      plan.a_kind = LD_BF16; plan.b_kind = LD_F32_AS_BF16; outN = H;
+      g.A = a; g.lda = lda; g.a_ks = 1; g.K = S; g.B0 = delta; g.ldb0 = 1; g.b_ks = H;
+      break;
+    case GLT_GEMM_EXPAND_WGRAD:  // out[S,H] = bf16(dy[M,S])^T . a[M,H]
+      plan.a_kind = LD_F32_AS_BF16; plan.b_kind = LD_BF16; outM = S; outN = H;
+      g.A = dy; g.lda = 1; g.a_ks = S; g.K = M; g.B0 = a; g.ldb0 = 1; g.b_ks = lda;
+      break;
+    case GLT_GEMM_CONTRACT_WGRAD:  // out[S,H] = a[M,S]^T . bf16(dy[M,H])
+      plan.a_kind = LD_BF16; plan.b_kind = LD_F32_AS_BF16; outM = S; outN = H;
+      g.A = a; g.lda = 1; g.a_ks = lda; g.K = M; g.B0 = dy; g.ldb0 = 1; g.b_ks = H;
+      break;
+    case GLT_GEMM_EXPAND_IGRAD:  // out[M,H] = bf16(dy[M,S]) . bf16(delta[S,H])
+      plan.a_kind = LD_F32_AS_BF16; plan.b_kind = LD_F32_AS_BF16; outN = H;
+      g.A = dy; g.lda = S; g.a_ks = 1; g.K = S; g.B0 = delta; g.ldb0 = 1; g.b_ks = H;
+      break;
+    default:  // CONTRACT_IGRAD: out[M,S] = bf16(dy[M,H]) . bf16(delta[S,H])^T
+      plan.a_kind = LD_F32_AS_BF16; plan.b_kind = LD_F32_AS_BF16; outN = S;
+      g.A = dy; g.lda = H; g.a_ks = 1; g.K = H; g.B0 = delta; g.ldb0 = H; g.b_ks = 1;
+      break;
+  }
+  GLT_CHECK(ldo >= outN, GLT_ERR_SHAPE, "glt_graft_gemm: ldo %lld < %d", (long long)ldo, outN);
+  g.n_hi = outN;
+  GProb p = prob(outM, outN, EPI_STORE, true, out, nullptr, nullptr, ldo);
+  p.alpha = alpha;
+  p.beta = beta;
+  plan.add_problem(p);
+  plan.add_seg(g);
+  if (outM == 0) return GLT_OK;
+  return run_gemm(plan, as_stream(stream), false);
+}
+
+}  // extern "C"

@@ -1,0 +1,250 @@
+"""Host-side operator surface of the grafted-SwiGLU path (Python mirror of
+the reference's graft ops / layer / bake / norm / RoPE / optimizer entry
+points), calling libglt.so through ctypes.
+
+torch tensors are used only as device memory and for the current stream;
+all arithmetic happens in the HIP kernels behind include/glt.h. Errors come
+back as glt_amd._ffi.GltError (the reference throws std::runtime_error,
+src/checks.hpp:10-18).
+"""
+import ctypes
+
+import torch
+
+from . import _ffi as F
+
+PROJ_GATE, PROJ_UP, PROJ_DOWN = 0, 1, 2
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dtype_code(dtype):
+    if dtype == torch.bfloat16:
+        return F.DTYPE_BF16
+    if dtype == torch.float32:
+        return F.DTYPE_F32
+    raise TypeError(f"unsupported dtype {dtype}")
+
+
+def delta_offset(layer_idx, proj_idx, slice_dim, h_slice_dim):
+    """Flat offset of (layer, projection) in [L*3, S, H] graft storage
+    (reference src/graft_ops_impl.inc:5-7)."""
+    return (layer_idx * 3 + proj_idx) * slice_dim * h_slice_dim
+
+
+class GraftSlice:
+    """One graft slice of one layer: placement + f32 masters [S,H] + the
+    packed bf16 mirror both orientations (reference GraftWeights,
+    src/types.hpp:190-201)."""
+
+    def __init__(self, i_start, s, h_start, h, gate=None, up=None, down=None):
+        self.i_start, self.s, self.h_start, self.h = int(i_start), int(s), int(h_start), int(h)
+        self.gate, self.up, self.down = gate, up, down
+        for t in (gate, up, down):
+            if t is not None:
+                assert t.dtype == torch.float32 and tuple(t.shape) == (self.s, self.h) and t.is_contiguous()
+        dev = next(t.device for t in (gate, up, down) if t is not None) if any(
+            t is not None for t in (gate, up, down)) else torch.device("cuda")
+        self.packed = torch.zeros(6 * self.s * self.h, dtype=torch.bfloat16, device=dev)
+
+    def c_struct(self):
+        return F.GraftSlice(self.i_start, self.s, self.h_start, self.h, _p(self.gate), _p(self.up), _p(self.down),
+                            _p(self.packed))
+
+    def pack(self):
+        """Refresh the bf16 mirror from the masters (reference
+        refresh_graft_weight_bf16, src/gemm_impl.inc:91-95)."""
+        s = self.c_struct()
+        F.call("glt_graft_pack", ctypes.byref(s), _p(self.packed), _stream())
+        return self
+
+
+def _slices_array(slices):
+    arr = (F.GraftSlice * max(1, len(slices)))()
+    for j, s in enumerate(slices):
+        arr[j] = s.c_struct()
+    return arr
+
+
+class BaseMLP:
+    """Frozen base weights of one MLP layer: gate/up [I,D], down [D,I], plus
+    the transposed copies the backward GEMMs read (made once)."""
+
+    def __init__(self, gate, up, down, prepare=True):
+        self.gate, self.up, self.down = gate, up, down
+        self.I, self.D = gate.shape
+        self.dtype = gate.dtype
+        self.gate_t = self.up_t = self.down_t = None
+        if prepare and self.I > 0:
+            self.prepare()
+
+    def prepare(self):
+        self.gate_t = torch.empty((self.D, self.I), dtype=self.dtype, device=self.gate.device)
+        self.up_t = torch.empty_like(self.gate_t)
+        self.down_t = torch.empty((self.I, self.D), dtype=self.dtype, device=self.gate.device)
+        d = F.MlpDesc(0, self.D, self.I, self.I, _dtype_code(self.dtype), 0, 0, None, None)
+        F.call("glt_base_prepare", ctypes.byref(d), _p(self.gate), _p(self.up), _p(self.down), _p(self.gate_t),
+               _p(self.up_t), _p(self.down_t), _stream())
+        return self
+
+    def c_struct(self):
+        return F.BaseWeights(_p(self.gate), _p(self.up), _p(self.down), _p(self.gate_t), _p(self.up_t),
+                             _p(self.down_t))
+
+
+def _desc(base, slices, M, N, explicit, recompute=False, state=None):
+    arr = _slices_array(slices)
+    flags = (F.MLP_EXPLICIT if explicit else 0) | (F.MLP_RECOMPUTE if recompute else 0)
+    d = F.MlpDesc(M, base.D, base.I, N, _dtype_code(base.dtype), flags, len(slices), arr,
+                  ctypes.pointer(state) if state is not None else None)
+    return d, arr
+
+
+def mlp_forward(base, slices, x, N, explicit=True, save=True):
+    """Grafted SwiGLU forward (reference forward_layer FFN section,
+    src/layer_forward_impl.inc:61-290). Returns y, gate_pre, up_pre, inter."""
+    M = x.shape[0]
+    d, keep = _desc(base, slices, M, N, explicit)
+    y = torch.empty((M, base.D), dtype=base.dtype, device=x.device)
+    inter = torch.empty((M, N), dtype=base.dtype, device=x.device)
+    g = torch.empty_like(inter) if save else None
+    u = torch.empty_like(inter) if save else None
+    b = base.c_struct()
+    F.call("glt_mlp_fwd", ctypes.byref(d), ctypes.byref(b), _p(x), _p(y), _p(g), _p(u), _p(inter), _stream())
+    return y, g, u, inter
+
+
+def mlp_backward_workspace(base, slices, M, N, explicit=True, recompute=False):
+    d, keep = _desc(base, slices, M, N, explicit, recompute)
+    return F.load().glt_mlp_bwd_workspace_size(ctypes.byref(d))
+
+
+def mlp_backward(base, slices, x, dy, N, gate_pre=None, up_pre=None, inter=None, want_dx=True, explicit=True,
+                 recompute=False, state=None, workspace=None):
+    """Graft-only backward (reference backward_layer FFN section,
+    src/layer_backward_impl.inc:10-361). Returns dx (f32) and per-slice
+    [gate, up, down] f32 gradients in [S,H] storage."""
+    M = x.shape[0]
+    d, keep = _desc(base, slices, M, N, explicit, recompute, state)
+    nbytes = F.load().glt_mlp_bwd_workspace_size(ctypes.byref(d))
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    dx = torch.empty((M, base.D), dtype=torch.float32, device=x.device) if want_dx else None
+    grads = []
+    garr = (F.GraftGrads * max(1, len(slices)))()
+    for j, s in enumerate(slices):
+        row = [torch.zeros((s.s, s.h), dtype=torch.float32, device=x.device) if t is not None else None
+               for t in (s.gate, s.up, s.down)]
+        grads.append(row)
+        garr[j] = F.GraftGrads(_p(row[0]), _p(row[1]), _p(row[2]))
+    b = base.c_struct()
+    F.call("glt_mlp_bwd", ctypes.byref(d), ctypes.byref(b), _p(x), _p(dy), _p(gate_pre), _p(up_pre), _p(inter),
+           _p(dx), garr, _p(workspace), nbytes, _stream())
+    return dx, grads
+
+
+def graft_gemm(kind, M, S, H, out, a=None, lda=0, delta=None, dy=None, ldo=None, alpha=1.0, beta=0.0):
+    """One of the reference's six graft GEMM kinds (src/config.hpp:31-38)."""
+    F.call("glt_graft_gemm", kind, M, S, H, _p(a), lda, _p(delta), _p(dy), _p(out),
+           ldo if ldo is not None else out.shape[-1], alpha, beta, _stream())
+    return out
+
+
+def rms_norm(x, w, eps):
+    """(y, variance) like the reference rms_norm (grafting.hip:116-146)."""
+    M, D = x.shape
+    y = torch.empty_like(x)
+    var = torch.empty(M, dtype=torch.float32, device=x.device)
+    F.call("glt_rmsnorm_fwd", _p(x), _p(w), _p(y), _p(var), M, D, eps, _stream())
+    return y, var
+
+
+def rms_norm_bwd(dy, x, w, var, eps):
+    """Reference rms_norm_bwd (grafting.hip:153-172); dy f32, returns dx f32."""
+    M, D = x.shape
+    dx = torch.empty((M, D), dtype=torch.float32, device=x.device)
+    F.call("glt_rmsnorm_bwd", _p(dy), _p(x), _p(w), _p(var), _p(dx), M, D, eps, _stream())
+    return dx
+
+
+def apply_rope(q, k, theta, pos_offset=0):
+    """In-place RoPE on q [B,T,nq,hd] and k [B,T,nk,hd] (reference apply_rope,
+    src/rope_impl.inc:8-39)."""
+    B, T, nq, hd = q.shape
+    nk = k.shape[2] if k is not None else 0
+    F.call("glt_rope_fwd", _p(q), nq, _p(k), nk, B, T, hd, theta, pos_offset, _stream())
+
+
+def adamw_step(w, g, m, v, step, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, clip_norm=0.0,
+               mirror=None):
+    """One AdamW step (reference adamw_fused_kernel + optional global clip)."""
+    n = w.numel()
+    ws_bytes = F.load().glt_adamw_workspace_size(n)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=w.device) if clip_norm > 0 else None
+    F.call("glt_adamw_step", _p(w), _p(g), _p(m), _p(v), _p(mirror), n, step, lr, beta1, beta2, eps, weight_decay,
+           clip_norm, _p(ws), ws_bytes if ws is not None else 0, _stream())
+
+
+def adamw_graft_step(slices, grads, m, v, step, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
+                     proj_mask=7):
+    """AdamW over graft slices with the packed-mirror refresh fused in.
+    grads/m/v: per slice a flat f32 [3*S*H] tensor (gate, up, down)."""
+    arr = _slices_array(slices)
+    F.call("glt_adamw_graft_step", arr, len(slices), F.ptr_array([g.data_ptr() for g in grads]),
+           F.ptr_array([t.data_ptr() for t in m]), F.ptr_array([t.data_ptr() for t in v]),
+           F.ptr_array([s.packed.data_ptr() for s in slices]), proj_mask, step, lr, beta1, beta2, eps,
+           weight_decay, _stream())
+
+
+def shadow_bake(state, gate, up, down, grafts, placements, *, D, I, N=None, materialize=False, gate_out=None,
+                up_out=None, down_out=None, layer_start=0, layer_end=None, proj_mask=7, graft_dtype=None):
+    """Bake graft deltas into bf16 base matrices (reference
+    apply_graft_to_shadow, src/shadow_bake_impl.inc:58-128).
+
+    gate/up/down: per-layer lists of bf16 tensors; grafts[j][l]: slice j's
+    flat [3,S,H] deltas for layer l; placements[j] = (i0, S, h0, H)."""
+    L = len(gate)
+    n_sl = len(placements)
+    if graft_dtype is None:
+        graft_dtype = grafts[0][0].dtype if n_sl else torch.float32
+    pl = (ctypes.c_int32 * max(1, 4 * n_sl))(*[int(v) for p in placements for v in p])
+    gptr = F.ptr_array([grafts[j][l].data_ptr() for j in range(n_sl) for l in range(L)])
+    d = F.BakeDesc(F.BAKE_MATERIALIZE if materialize else F.BAKE_IN_PLACE, L, layer_start,
+                   L - 1 if layer_end is None else layer_end, proj_mask, D, I, N if N is not None else I,
+                   _dtype_code(graft_dtype), n_sl, pl, gptr)
+
+    def arr(ts):
+        return F.ptr_array([t.data_ptr() for t in ts]) if ts is not None else None
+
+    F.call("glt_shadow_bake", ctypes.byref(d), ctypes.byref(state), arr(gate), arr(up), arr(down), arr(gate_out),
+           arr(up_out), arr(down_out), _stream())
+
+
+def f32_to_bf16(x):
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    F.call("glt_f32_to_bf16", _p(x), _p(out), x.numel(), _stream())
+    return out
+
+
+def fill_normal(t, seed, tensor_id, mean=0.0, std=1.0):
+    F.call("glt_fill_normal", _p(t), _dtype_code(t.dtype), t.numel(), seed, tensor_id, mean, std, _stream())
+    return t
+
+
+def silu_mul(g, u):
+    out = torch.empty_like(g)
+    F.call("glt_silu_mul", _p(g), _p(u), _p(out), g.numel(), _stream())
+    return out
+
+
+def gate_up_bwd(gi, g, u):
+    dg = torch.empty(gi.shape, dtype=torch.float32, device=gi.device)
+    du = torch.empty_like(dg)
+    F.call("glt_gate_up_bwd", _p(gi), _p(g), _p(u), _p(dg), _p(du), gi.numel(), _stream())
+    return dg, du

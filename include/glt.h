@@ -1,0 +1,320 @@
+/*
+ * glt.h — C ABI of the MI355X (gfx950) grafted-SwiGLU layer path.
+ *
+ * Every entry point takes caller-owned device buffers, explicit shapes and an
+ * explicit HIP stream (hipStream_t passed as void*, NULL = default stream),
+ * and returns an int status. No C++ exception crosses this boundary and no
+ * entry point allocates device memory; scratch space is passed in by the
+ * caller (glt_mlp_bwd_workspace_size tells how much).
+ *
+ * bf16 values are passed as their 16-bit patterns (uint16_t storage).
+ * All matrices are row-major. "[R,C]" means R rows of C contiguous elements.
+ *
+ * The reference implements this path as an internal C++ API with shapes held
+ * in a process-global config (reference src/config.hpp:40-95, g_cfg). Here the
+ * shapes travel in descriptors instead. Citations name the reference function
+ * each entry point replaces.
+ */
+#ifndef GLT_H_
+#define GLT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLT_ABI_VERSION 1
+
+/* ------------------------------------------------------------------ status */
+typedef int32_t glt_status;
+#define GLT_OK                     0
+#define GLT_ERR_INVALID_ARG        1  /* null pointer / bad enum / bad flag        */
+#define GLT_ERR_SHAPE              2  /* inconsistent or out-of-range dimensions   */
+#define GLT_ERR_DTYPE              3  /* unsupported dtype combination             */
+#define GLT_ERR_ALIGNMENT          4  /* pointer or stride alignment not met       */
+#define GLT_ERR_WORKSPACE          5  /* workspace missing or too small            */
+#define GLT_ERR_ALREADY_BAKED      6  /* second bake on the same model state       */
+#define GLT_ERR_BAKED_NO_BACKWARD  7  /* backward on a shadow-baked model          */
+#define GLT_ERR_HIP                8  /* a HIP runtime call failed                 */
+#define GLT_ERR_UNSUPPORTED        9  /* valid request this build does not serve   */
+
+/* ------------------------------------------------------------------ dtypes */
+#define GLT_DTYPE_BF16 0
+#define GLT_DTYPE_F32  1
+
+/* Projection indices, as in the reference flat graft storage
+ * (reference src/graft_ops_impl.inc:5-7: offset = (layer*3 + proj)*S*H). */
+#define GLT_PROJ_GATE 0
+#define GLT_PROJ_UP   1
+#define GLT_PROJ_DOWN 2
+#define GLT_PROJ_MASK_ALL 7 /* bit p set = projection p grafted */
+
+/* Shadow-bake guard state, owned by the caller (one per model instance).
+ * Replaces the process-global g_shadow_baked (reference src/shadow_bake.hpp:5). */
+typedef struct {
+  int32_t baked; /* 0 = not baked; set to 1 by a successful glt_shadow_bake */
+} glt_model_state;
+
+/* One graft slice of one layer.
+ *
+ * Placement (reference src/shadow_bake_impl.inc:11-14, docs/contract_audit.md:601-612):
+ *   gate/up delta [S,H] adds onto rows [i_start, i_start+S) x cols [h_start, h_start+H)
+ *   of W_gate / W_up ([N,D]); the down delta is stored [S,H] too and adds onto
+ *   the transposed block rows [h_start, h_start+H) x cols [i_start, i_start+S)
+ *   of W_down ([D,N]).
+ * An "appended" slice (i_start >= I) lives in the zero-extended tail of the
+ * base, i.e. it adds new neurons; an in-place slice (i_start+S <= I) adds onto
+ * existing ones (the reference's domain-sliced form).
+ *
+ * master_*: f32 [S,H] master deltas (reference GraftWeights.d_weight,
+ *           src/types.hpp:190-201). NULL = projection not grafted.
+ * packed:   bf16 mirror written by glt_graft_pack / glt_adamw_step, 6*S*H
+ *           elements: gate[S,H], gate^T[H,S], up[S,H], up^T[H,S],
+ *           down[S,H], down^T[H,S]. Read by the bf16 path; unused by f32.  */
+typedef struct {
+  int32_t i_start, s, h_start, h;
+  const float* master_gate;
+  const float* master_up;
+  const float* master_down;
+  const uint16_t* packed;
+} glt_graft_slice;
+
+/* Per-slice f32 weight-gradient outputs of glt_mlp_bwd, [S,H] each in the
+ * same storage orientation as the master (reference d_delta_grad,
+ * src/graft_ops_impl.inc:120-141, :214-228). NULL = not requested. */
+typedef struct {
+  float* gate;
+  float* up;
+  float* down;
+} glt_graft_grads;
+
+/* Frozen base weights of one MLP layer (torch Linear [out,in] layout).
+ * gate/up [I,D], down [D,I]. The *_t copies are the transposes used by the
+ * backward GEMMs (gate_t/up_t [D,I], down_t [I,D]); glt_base_prepare makes
+ * them once per frozen base. dtype = the path dtype. */
+typedef struct {
+  const void* gate;
+  const void* up;
+  const void* down;
+  const void* gate_t;
+  const void* up_t;
+  const void* down_t;
+} glt_base_weights;
+
+/* Shape of one grafted SwiGLU MLP call.
+ *   M tokens, D hidden, I base intermediate rows held by W_gate/W_up,
+ *   N >= I total neurons (rows [I,N) of the base are zero: appended grafts).
+ * flags: GLT_MLP_EXPLICIT applies the slices (the reference's
+ * use_explicit_graft, src/layer_forward_impl.inc:76); without it the call is
+ * the plain base MLP (e.g. over shadow-baked weights). */
+#define GLT_MLP_EXPLICIT 1
+/* GLT_MLP_RECOMPUTE: glt_mlp_bwd recomputes gate_pre/up_pre/inter from x in
+ * its workspace instead of reading saved activations (the reference's
+ * recompute_ffn, src/layer_recompute_impl.inc:8-91). */
+#define GLT_MLP_RECOMPUTE 2
+typedef struct {
+  int32_t M, D, I, N;
+  int32_t dtype;   /* GLT_DTYPE_BF16 or GLT_DTYPE_F32 */
+  int32_t flags;
+  int32_t n_slices;
+  const glt_graft_slice* slices;
+  glt_model_state* state; /* nullable; checked for the baked guard in backward */
+} glt_mlp_desc;
+
+/* ----------------------------------------------------------- library info */
+int32_t glt_version(void);                 /* GLT_ABI_VERSION */
+const char* glt_last_error_string(void);   /* thread-local text of the last error */
+/* Device properties the roofline needs: CU count and peak engine clock (MHz). */
+glt_status glt_device_info(int32_t device, int32_t* cu_count, int32_t* clock_mhz,
+                           int64_t* hbm_bytes);
+
+/* Launch timing. While enabled, each kernel launch of the library is
+ * bracketed by HIP events on its own stream, keyed by a label naming the
+ * kernel's role ("gate_up", "down", "dinter", "dx", "wgrad", "bake", ...).
+ * Replaces the reference's --profile-graft-gemms (src/gemm_impl.inc:153-199,
+ * :408-444) without its synchronisation after every GEMM.
+ * glt_profile_collect waits for the recorded events, writes up to
+ * max_labels NUL-separated labels into names, their summed milliseconds and
+ * launch counts, clears the records and returns the number of labels. */
+glt_status glt_profile_enable(int32_t on);
+int32_t glt_profile_collect(char* names, size_t names_len, double* total_ms, int64_t* counts,
+                            int32_t max_labels);
+
+/* ------------------------------------------------------------ conversions */
+/* out[i] = RNE bf16 of in[i] (reference f32_to_bf16_kernel, src/gemm_impl.inc:69-89). */
+glt_status glt_f32_to_bf16(const float* in, uint16_t* out, int64_t n, void* stream);
+
+/* Synthetic inputs: counter-based normal generator keyed by (seed, tensor_id):
+ * splitmix64 -> Box-Muller in f64 -> f32 (-> RNE bf16). out[i] = mean + std*z_i.
+ * Not a reference function (the reference loads real weights); used so that
+ * benchmarks and host checks can draw the same inputs. */
+glt_status glt_fill_normal(void* out, int32_t dtype, int64_t n, uint64_t seed,
+                           uint64_t tensor_id, double mean, double stdev,
+                           void* stream);
+
+/* --------------------------------------------------------------- graft ops */
+/* Build the bf16 mirror of one slice (both orientations) from its f32 masters.
+ * Replaces refresh_graft_weight_bf16 / convert_f32_to_bf16 of the reference
+ * (src/gemm_impl.inc:85-95), which it ran before every graft GEMM call. */
+glt_status glt_graft_pack(const glt_graft_slice* slice, uint16_t* packed, void* stream);
+
+/* Transposed copies of a frozen base (dst[c,r] = src[r,c]), rows x cols. */
+glt_status glt_transpose(const void* src, void* dst, int32_t rows, int32_t cols,
+                         int32_t dtype, void* stream);
+glt_status glt_base_prepare(const glt_mlp_desc* d, const void* gate, const void* up,
+                            const void* down, void* gate_t, void* up_t, void* down_t,
+                            void* stream);
+
+/* The six graft GEMM kinds of the reference (src/config.hpp:31-38,
+ * graft_gemm_fwd / grad_gemm / grad_gemm_storage_canonical
+ * src/gemm_impl.inc:388-584, graft ops src/graft_ops_impl.inc:14-228).
+ * All operands bf16 except out (f32) and delta (f32 master, rounded to bf16
+ * per call exactly as the reference does). S,H = slice dims; M = tokens.
+ *   0 EXPAND_FWD      out[M,S]  = a[M,H](lda) . bf16(delta[S,H])^T
+ *   1 CONTRACT_FWD    out[M,H]  = a[M,S](lda) . bf16(delta[S,H])
+ *   2 EXPAND_WGRAD    out[S,H]  = bf16(dy[M,S])^T . a[M,H](lda)      dy f32
+ *   3 CONTRACT_WGRAD  out[S,H]  = a[M,S](lda)^T . bf16(dy[M,H])      dy f32
+ *   4 EXPAND_IGRAD    out[M,H]  = bf16(dy[M,S]) . bf16(delta[S,H])  dy f32
+ *   5 CONTRACT_IGRAD  out[M,S]  = bf16(dy[M,H]) . bf16(delta[S,H])^T dy f32
+ * out = alpha*result + beta*out, with row stride ldo. */
+#define GLT_GEMM_EXPAND_FWD     0
+#define GLT_GEMM_CONTRACT_FWD   1
+#define GLT_GEMM_EXPAND_WGRAD   2
+#define GLT_GEMM_CONTRACT_WGRAD 3
+#define GLT_GEMM_EXPAND_IGRAD   4
+#define GLT_GEMM_CONTRACT_IGRAD 5
+glt_status glt_graft_gemm(int32_t kind, int32_t M, int32_t S, int32_t H,
+                          const uint16_t* a, int64_t lda, const float* delta,
+                          const float* dy, float* out, int64_t ldo, float alpha,
+                          float beta, void* stream);
+
+/* ------------------------------------------------------------- MLP layer */
+/* Forward of the grafted SwiGLU MLP (reference FFN section of forward_layer,
+ * src/layer_forward_impl.inc:61-290, with execute_expand_forward /
+ * execute_contract_forward src/graft_ops_impl.inc:14-114):
+ *   gate_pre = x . [W_gate (+) grafts]^T, up_pre likewise      [M,N]
+ *   inter    = silu(gate_pre) * up_pre                          [M,N]
+ *   y        = inter . [W_down (+) grafts]^T                    [M,D]
+ * bf16 path: one concat-N MFMA GEMM for gate/up with the SiLU*up epilogue and
+ * one K-concat GEMM for down, graft terms accumulated in fp32.
+ * gate_pre/up_pre: saved for glt_mlp_bwd (nullable: then backward recomputes).
+ * inter: required. Buffers are [M,N] / [M,D] of the path dtype. */
+glt_status glt_mlp_fwd(const glt_mlp_desc* d, const glt_base_weights* w,
+                       const void* x, void* y, void* gate_pre, void* up_pre,
+                       void* inter, void* stream);
+
+/* Graft-only backward (reference FFN section of backward_layer,
+ * src/layer_backward_impl.inc:10-361; base weights frozen):
+ *   dInter = dy . W_down_ext ; dgate/dup via the SiLU*up derivative;
+ *   grads[j] = per-slice dW (f32, [S,H] storage); dx = d(x) f32 [M,D].
+ * dy is [M,D] of the path dtype. dx nullable. Returns
+ * GLT_ERR_BAKED_NO_BACKWARD when d->state says the model is shadow-baked
+ * (reference src/layer_backward_impl.inc:11-13). */
+size_t glt_mlp_bwd_workspace_size(const glt_mlp_desc* d);
+glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w,
+                       const void* x, const void* dy, const void* gate_pre,
+                       const void* up_pre, const void* inter, float* dx,
+                       const glt_graft_grads* grads, void* ws, size_t ws_bytes,
+                       void* stream);
+
+/* Unfused parity probes of the elementwise stages.
+ * glt_silu_mul:  out = bf16(g*sigmoid(g)*u)   (reference fused_silu_product_kernel,
+ *                src/kernels_elementwise_impl.inc:378-448)
+ * glt_gate_up_bwd: dg = gi*u*s*(1+g*(1-s)), du = gi*g*s, f32 out
+ *                (reference fused_gate_up_bwd_kernel, :80-124) */
+glt_status glt_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n,
+                        void* stream);
+glt_status glt_gate_up_bwd(const float* gi, const uint16_t* g, const uint16_t* u,
+                           float* dg, float* du, int64_t n, void* stream);
+
+/* --------------------------------------------------------------- RMSNorm */
+/* y = bf16(x * rsqrt(var+eps) * w), var[m] = mean(x^2) (mean-square, as the
+ * reference stores it). x,y [M,D] bf16, w [D] bf16, var [M] f32.
+ * Reference rms_norm / rms_norm_fwd_kernel (grafting.hip:116-146,
+ * src/kernels_rmsnorm_kernels.inc:8-60). */
+glt_status glt_rmsnorm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* y, float* var,
+                           int32_t M, int32_t D, float eps, void* stream);
+/* dx = dy*r*w - x*mean(dy*x*w)*r^3, r = rsqrt(var+eps); dy,dx f32 [M,D].
+ * Reference rms_norm_bwd / rms_norm_bwd_kernel (grafting.hip:153-172,
+ * src/kernels_rmsnorm_kernels.inc:70-126). */
+glt_status glt_rmsnorm_bwd(const float* dy, const uint16_t* x, const uint16_t* w,
+                           const float* var, float* dx, int32_t M, int32_t D, float eps,
+                           void* stream);
+
+/* ------------------------------------------------------------------- RoPE */
+/* In-place rotate-half RoPE on q [B,T,n_q_heads,head_dim] and k
+ * [B,T,n_kv_heads,head_dim] (bf16; k nullable), positions pos_offset + t.
+ * Reference apply_rope (src/rope_impl.inc:8-39): inv_freq_i = 1/theta^(2i/hd)
+ * and angles in f32, cos/sin rounded to bf16, r1 = x1*c - x2*s,
+ * r2 = x2*c + x1*s. Here the rotation runs in f32 with one rounding per
+ * output. The caller skips layers its no-RoPE mask excludes
+ * (reference src/layer_forward_impl.inc:37-39). */
+glt_status glt_rope_fwd(uint16_t* q, int32_t n_q_heads, uint16_t* k, int32_t n_kv_heads,
+                        int32_t B, int32_t T, int32_t head_dim, float theta,
+                        int32_t pos_offset, void* stream);
+
+/* ------------------------------------------------------------------ AdamW */
+/* One AdamW step over n f32 params (reference adamw_fused_kernel,
+ * src/kernels_optimizer_impl.inc:11-77) with bias corrections for step
+ * (0-based, as the reference's step+1). clip_norm > 0 first scales grads to
+ * global L2 norm <= clip_norm using sqrt(sum g^2 + 1e-8) (reference
+ * reduce_l2/calc_scale/apply_scale, src/kernels_elementwise_impl.inc:133-213);
+ * clip_norm <= 0 = no clip. The clip needs ws of glt_adamw_workspace_size(n)
+ * bytes. bf16_mirror (nullable) receives bf16(w). */
+size_t glt_adamw_workspace_size(int64_t n);
+glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* bf16_mirror,
+                          int64_t n, int32_t step, float lr, float beta1, float beta2,
+                          float eps, float weight_decay, float clip_norm, void* ws,
+                          size_t ws_bytes, void* stream);
+
+/* AdamW over a whole graft set with the packed-mirror refresh fused in:
+ * updates each slice's masters (treated as writable) and rewrites its
+ * packed bf16 mirror in both orientations. grads/m/v are per-slice [3,S,H]
+ * f32 buffers laid out gate,up,down. proj_mask as in the reference
+ * (skipped projections are untouched, src/kernels_optimizer_impl.inc:20-25). */
+glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
+                                float* const* grads, float* const* m, float* const* v,
+                                uint16_t* const* packed_out, int32_t proj_mask,
+                                int32_t step, float lr, float beta1, float beta2,
+                                float eps, float weight_decay, void* stream);
+
+/* ------------------------------------------------------------ shadow bake */
+/* Merge graft deltas into bf16 base matrices (reference shadow_bake_kernel /
+ * apply_graft_to_shadow, src/shadow_bake_impl.inc:15-128).
+ *
+ * mode GLT_BAKE_IN_PLACE: base[l] += delta, in place (reference semantics);
+ *   gate/up base [I,D] (row stride D), down base [D,I] (row stride I).
+ * mode GLT_BAKE_MATERIALIZE: out[l] = zero-extended base (+) deltas, with
+ *   gate/up out [N,D] and down out [D,N]; base matrices are read only.
+ * Every output element is one RNE of f32(base) + f32(delta): bit-exact.
+ *
+ * graft[l] points at layer l's flat [3,S,H] deltas (gate, up, down) of the
+ * given dtype, i.e. the reference's d_weight + delta_offset(l, 0).
+ * Layers outside [layer_start, layer_end] and projections not in proj_mask
+ * are skipped (reference should_graft_layer / should_graft_proj,
+ * src/config.hpp:100-110). A second bake on the same state fails with
+ * GLT_ERR_ALREADY_BAKED (reference src/shadow_bake_impl.inc:59-62). */
+#define GLT_BAKE_IN_PLACE    0
+#define GLT_BAKE_MATERIALIZE 1
+typedef struct {
+  int32_t mode;
+  int32_t num_layers;
+  int32_t layer_start, layer_end; /* inclusive */
+  int32_t proj_mask;
+  int32_t D, I, N;                /* N used by MATERIALIZE (N >= I) */
+  int32_t graft_dtype;            /* GLT_DTYPE_F32 (master) or GLT_DTYPE_BF16 */
+  int32_t n_slices;               /* slices baked together (stacked grafts) */
+  const int32_t* placement;       /* n_slices x {i_start, s, h_start, h} */
+  const void* const* graft;       /* [n_slices * num_layers] flat [3,S,H] per layer */
+} glt_bake_desc;
+glt_status glt_shadow_bake(const glt_bake_desc* d, glt_model_state* state,
+                           void* const* gate, void* const* up, void* const* down,
+                           void* const* gate_out, void* const* up_out,
+                           void* const* down_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GLT_H_ */

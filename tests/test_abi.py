@@ -1,0 +1,55 @@
+"""The C-ABI library loads and exports every entry point include/glt.h
+declares (no GPU calls)."""
+import ctypes
+import os
+import re
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "glt.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(glt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_surface():
+    names = declared_functions()
+    for n in ("glt_mlp_fwd", "glt_mlp_bwd", "glt_shadow_bake", "glt_rmsnorm_fwd", "glt_rmsnorm_bwd", "glt_rope_fwd",
+              "glt_adamw_step", "glt_graft_gemm", "glt_silu_mul", "glt_gate_up_bwd", "glt_f32_to_bf16"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from glt_amd import _ffi
+    lib = ctypes.CDLL(_ffi.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(declared_functions()) == set(_ffi.SIGNATURES), "ctypes binding out of sync with glt.h"
+
+
+def test_version_and_error_string():
+    from glt_amd import _ffi
+    lib = _ffi.load()
+    assert lib.glt_version() == 1
+    assert isinstance(lib.glt_last_error_string(), bytes)
+
+
+def test_host_validation_errors_without_gpu():
+    """Descriptor checks run before any GPU call and return distinct codes."""
+    from glt_amd import _ffi as F
+    lib = F.load()
+    st = F.ModelState(1)
+    d = F.MlpDesc(16, 64, 64, 64, F.DTYPE_BF16, F.MLP_EXPLICIT, 0, None, ctypes.pointer(st))
+    w = F.BaseWeights(1, 1, 1, 1, 1, 1)
+    rc = lib.glt_mlp_bwd(ctypes.byref(d), ctypes.byref(w), 1, 1, 1, 1, 1, None, None, None, 0, None)
+    assert rc == 7  # GLT_ERR_BAKED_NO_BACKWARD (reference src/layer_backward_impl.inc:11-13)
+    bd = F.BakeDesc(0, 1, 0, 0, 7, 64, 64, 64, F.DTYPE_F32, 0, None, None)
+    assert lib.glt_shadow_bake(ctypes.byref(bd), ctypes.byref(st), None, None, None, None, None, None, None) == 6
+    d2 = F.MlpDesc(16, 64, 128, 64, F.DTYPE_BF16, 0, 0, None, None)  # N < I
+    assert lib.glt_mlp_fwd(ctypes.byref(d2), ctypes.byref(w), 1, 1, None, None, 1, None) == 2
+    d3 = F.MlpDesc(16, 64, 64, 64, 7, 0, 0, None, None)
+    assert lib.glt_mlp_fwd(ctypes.byref(d3), ctypes.byref(w), 1, 1, None, None, 1, None) == 3
+    assert lib.glt_rmsnorm_fwd(None, None, None, None, -1, 8, 1e-5, None) == 2
+    assert lib.glt_graft_gemm(9, 1, 1, 1, None, 0, None, None, None, 0, 1.0, 0.0, None) == 1
+    assert lib.glt_adamw_step(1, 1, 1, 1, None, 10, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1.0, None, 0, None) == 5

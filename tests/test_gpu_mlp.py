@@ -1,0 +1,138 @@
+"""GPU parity of the grafted SwiGLU MLP forward/backward against the oracle.
+
+Shapes are chosen so the oracle finishes in seconds: aligned bf16 shapes
+run the gfx950 MFMA kernel, the f32 and unaligned shapes the generic kernel.
+"""
+import numpy as np
+import pytest
+
+from helpers import (assert_bf16_budget, assert_f32_close, draw, make_layer, rel_l2, to_dev, to_np)
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(dev, D, I, N, pl, M, bf16, explicit=True, recompute=False, seed_x=100):
+    import torch
+    from glt_amd import ops, synth
+    dt = torch.bfloat16 if bf16 else torch.float32
+    wg, wu, wd, sl = make_layer(D, I, N, pl, bf16)
+    x = draw((M, D), seed_x, synth.TID_X, 0, 1, bf16)
+    dy = draw((M, D), 200, synth.TID_DY, 0, 1, bf16)
+    base = ops.BaseMLP(to_dev(wg, dt), to_dev(wu, dt), to_dev(wd, dt))
+    gs = []
+    for s in sl:
+        g = ops.GraftSlice(s["i0"], s["s"], s["h0"], s["h"], *(to_dev(s[p], torch.float32) for p in ("gate", "up", "down")))
+        gs.append(g.pack())
+    xd, dyd = to_dev(x, dt), to_dev(dy, dt)
+    y, gp, up, inter = ops.mlp_forward(base, gs, xd, N, explicit=explicit)
+    dx, grads = ops.mlp_backward(base, gs, xd, dyd, N, gp, up, inter, explicit=explicit, recompute=recompute)
+    torch.cuda.synchronize()
+    osl = sl if explicit else []
+    rg, ru, ri, ry = O.mlp_fwd(x, wg, wu, wd, N, osl, bf16=bf16)
+    rdx, rgrads = O.mlp_bwd(x, wg, wu, wd, N, osl, rg, ru, ri, dy, bf16=bf16)
+    return dict(y=(to_np(y), ry), g=(to_np(gp), rg), u=(to_np(up), ru), inter=(to_np(inter), ri),
+                dx=(to_np(dx), rdx), grads=[[to_np(t) if t is not None else None for t in row] for row in grads],
+                rgrads=rgrads)
+
+
+@pytest.mark.parametrize("M,D,I,S", [(256, 256, 512, 128), (512, 512, 1024, 256)])
+def test_mfma_appended_bf16(dev, M, D, I, S):
+    """BASELINE's appended form (new neurons after the base rows) on the MFMA path."""
+    N = I + S
+    r = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=True)
+    for k, q in (("g", 2), ("u", 2), ("inter", 3), ("y", 4)):
+        assert_bf16_budget(*r[k], q=q, what=k)
+    assert_bf16_budget(*r["dx"], q=4, what="dx")
+    for p, name in enumerate(("gate", "up", "down")):
+        assert_bf16_budget(r["grads"][0][p], r["rgrads"][0][p], q=4, what=f"dW_{name}")
+
+
+def test_mfma_inplace_and_stacked_bf16(dev):
+    """In-place slices (domain-sliced, the reference's CLI form) plus an
+    appended slice, all on the MFMA path (64-aligned)."""
+    M, D, I, N = 256, 512, 1024, 1152
+    pl = [(0, 128, 0, 256), (512, 256, 256, 256), (1024, 128, 64, 448)]
+    r = _run(dev, D, I, N, pl, M, bf16=True)
+    for k, q in (("g", 2), ("u", 2), ("inter", 3), ("y", 4), ("dx", 4)):
+        assert_bf16_budget(*r[k], q=q, what=k)
+    for j in range(len(pl)):
+        for p in range(3):
+            assert_bf16_budget(r["grads"][j][p], r["rgrads"][j][p], q=4, what=f"slice{j} proj{p}")
+
+
+def test_f32_config1(dev):
+    """Config 1: hidden 512, base 1408, 256 appended neurons, 4x128 tokens, fp32."""
+    M, D, I, S = 512, 512, 1408, 256
+    N = I + S
+    r = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=False)
+    for k in ("g", "u", "inter", "y", "dx"):
+        assert_f32_close(*r[k], tol=1e-5, what=k)
+    for p in range(3):
+        assert_f32_close(r["grads"][0][p], r["rgrads"][0][p], tol=1e-5, what=f"dW{p}")
+
+
+def test_unaligned_bf16_generic(dev):
+    """Odd slice placements (H=513-style) go through the generic kernel."""
+    M, D, I, N = 70, 100, 130, 150
+    pl = [(3, 17, 5, 33), (130, 20, 0, 100)]
+    r = _run(dev, D, I, N, pl, M, bf16=True)
+    for k, q in (("g", 2), ("u", 2), ("inter", 3), ("y", 4), ("dx", 4)):
+        assert_bf16_budget(*r[k], q=q, what=k)
+
+
+def test_recompute_matches_saved(dev):
+    import torch
+    M, D, I, S = 256, 256, 512, 128
+    N = I + S
+    a = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=True, recompute=False)
+    b = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=True, recompute=True)
+    np.testing.assert_array_equal(a["dx"][0], b["dx"][0])
+    for p in range(3):
+        np.testing.assert_array_equal(a["grads"][0][p], b["grads"][0][p])
+
+
+def test_explicit_off_is_base_only(dev):
+    """use_explicit_graft=false: slices are ignored (reference
+    src/layer_forward_impl.inc:76)."""
+    M, D, I, S = 128, 256, 512, 128
+    N = I + S
+    r = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=True, explicit=False)
+    assert_bf16_budget(*r["y"], q=4, what="y")
+    assert np.all(r["inter"][0][:, I:] == 0)
+
+
+def test_test6_f32_explicit_equals_baked(dev):
+    """Reference tests/test6_stack_vs_bake_f32.cpp:43-58,199-205: two domains
+    (S=3, H=2) in a D=4, F=6 base; explicit injection == baked weights,
+    tol 1e-4 abs or 1e-6 rel."""
+    import torch
+    from glt_amd import ops
+    S, H, D, F, M = 3, 2, 4, 6, 2
+    gate0 = np.array([(i + 1) * 0.1 for i in range(F * D)], np.float32).reshape(F, D)
+    up0 = np.array([(i + 1) * 0.07 for i in range(F * D)], np.float32).reshape(F, D)
+    down0 = np.array([(i + 1) * 0.05 for i in range(D * F)], np.float32).reshape(D, F)
+    x = np.arange(1, 9, dtype=np.float32).reshape(M, D)
+
+    def mk(b, stp):
+        return np.array([[b + i * stp + j for j in range(H)] for i in range(S)], np.float32)
+
+    g0, g1, u0, u1, d0, d1 = mk(0.5, 0.1), mk(0.3, 0.2), mk(0.9, 0.15), mk(0.7, 0.05), mk(1.2, 0.08), mk(1.0, 0.12)
+    dt = torch.float32
+    base = ops.BaseMLP(to_dev(gate0, dt), to_dev(up0, dt), to_dev(down0, dt))
+    gs = [ops.GraftSlice(0, S, 0, H, *(to_dev(a, dt) for a in (g0, u0, d0))).pack(),
+          ops.GraftSlice(S, S, H, H, *(to_dev(a, dt) for a in (g1, u1, d1))).pack()]
+    y, gp, up, inter = ops.mlp_forward(base, gs, to_dev(x, dt), F)
+    # baked weights (path B of the reference test)
+    gb, ub, db = gate0.copy(), up0.copy(), down0.copy()
+    gb[0:S, 0:H] += g0; gb[S:2 * S, H:2 * H] += g1
+    ub[0:S, 0:H] += u0; ub[S:2 * S, H:2 * H] += u1
+    db[0:H, 0:S] += d0.T; db[H:2 * H, S:2 * S] += d1.T
+    baked = ops.BaseMLP(to_dev(gb, dt), to_dev(ub, dt), to_dev(db, dt))
+    yb, gpb, upb, interb = ops.mlp_forward(baked, [], to_dev(x, dt), F, explicit=False)
+    torch.cuda.synchronize()
+    for a, b, nm in ((gp, gpb, "gate_pre"), (up, upb, "up_pre"), (inter, interb, "inter"), (y, yb, "ffn_out")):
+        a, b = to_np(a), to_np(b)
+        md = np.max(np.abs(a - b))
+        mv = np.max(np.maximum(np.abs(a), np.abs(b)))
+        assert md < 1e-4 or md / mv < 1e-6, (nm, md, mv)
