@@ -86,23 +86,37 @@ __device__ __forceinline__ bool seg_hits(const GSeg& S, const GProb& P, int n0, 
 // =========================================================================
 // gfx950 MFMA kernel: bf16 x bf16 -> f32, v_mfma_f32_32x32x16_bf16.
 //
-// Workgroup tile 256 (M) x 256 B-rows x 64 (K), 4 wavefronts in a 2x2
-// arrangement; each wavefront owns 128x128 outputs = 4x4 MFMA 32x32 tiles
-// (256 fp32 accumulators per lane). Plain form: the 256 B-rows are 256
-// output columns. Dual form: B-rows [0,128) are gate rows and [128,256) the
-// up rows of the same 128 output columns.
+// Workgroup tile 256 (M) x 256 B-rows, K in steps of 32, 4 wavefronts in a
+// 2x2 arrangement; each wavefront owns 128x128 outputs = 4x4 MFMA 32x32
+// tiles (256 fp32 accumulators per lane, in AGPRs). Plain form: the 256
+// B-rows are 256 output columns. Dual form: B-rows [0,128) are gate rows and
+// [128,256) the up rows of the same 128 output columns.
 //
-// Global -> LDS: 16-byte raw buffer loads (out-of-range rows read as zero),
-// staged through registers one K-step ahead, LDS double buffered (2 x 64 KB).
-// LDS rows are 128 bytes; the 16-byte chunk index is XOR-swizzled with the
-// row so both the row-wise stores and the MFMA fragment reads (32 rows x
-// one chunk) spread over all banks.
+// Global -> LDS: direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds):
+// each wavefront instruction moves 1 KB (8 rows x 128 bytes) straight into
+// LDS, lane L landing at base + 16*L; rows outside a tile's valid range get
+// an out-of-range offset and arrive as zeros. Two 64 KB stages alternate;
+// the loads of step it+1 are issued as soon as the barrier late in step it-1
+// frees their stage, a full K-step ahead of their use, and no VGPRs or
+// ds_write instructions carry the tiles.
 // =========================================================================
 constexpr int kBM = 256, kBK = 64;
-constexpr int kTileElems = kBM * kBK;              // one operand tile
-constexpr size_t kMfmaLds = 2 * 2 * kTileElems * 2;  // 2 buffers x (A,B) x bf16
+constexpr int kStages = 2;
+constexpr int kTileElems = kBM * kBK;                    // one operand tile
+constexpr int kStageElems = 2 * kTileElems;              // A then B
+constexpr size_t kMfmaLds = (size_t)kStages * kStageElems * 2;  // 128 KB
 
-__device__ __forceinline__ int swz(int row, int kc) { return row * kBK + ((kc ^ (row & 7)) << 3); }
+// Rows are 64 bf16 = 128 bytes, one cache line each, so every global
+// request a tile issues moves a whole line. gfx950 LDS serves a
+// 16-byte-per-lane access 16 lanes at a time over 64 banks (256 bytes); a
+// 16-lane group reading one logical chunk of 16 consecutive rows touches
+// bank group 8*(row&1) + physical chunk, so the physical chunk is the
+// logical one XOR (row>>1)&7, which makes the 16 groups distinct.
+__device__ __forceinline__ int swz_key(int row) { return (row >> 1) & 7; }
+
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n and leaves
+// expcnt / lgkmcnt unconstrained.
+constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 constexpr int kEpPitch = 132;  // f32 words per staged epilogue row (128 + pad)
 
@@ -192,7 +206,8 @@ template <typename TO, int MODE, bool DUAL>
 __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   constexpr int BN = DUAL ? 128 : 256;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   int tm, tn;
   const int pi = locate_tile(args, tm, tn, true);
@@ -206,40 +221,65 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
     return s;
   };
 
-  u32x4 ra[8], rb[8];
-  auto gload = [&](int s, int k0) {
+  // ---- load side. Per K-step each wavefront issues 8 A and 8 B
+  // direct-to-LDS loads: instruction i of wave w fills tile rows
+  // 8*g .. 8*g+7 with g = 4*i + w; lane L takes row 8*g + L/8 and physical
+  // chunk L&7, i.e. logical chunk (L&7) ^ swz_key(row). Buffer descriptors
+  // and per-lane byte offsets are set once per segment; the K position rides
+  // in the scalar offset.
+  __amdgpu_buffer_rsrc_t rA, rB0, rB1;
+  uint32_t voA[8], voB[8];
+  auto setup = [&](int s) {
     const GSeg& S = args.s[s];
-    const __amdgpu_buffer_rsrc_t rA = make_rsrc(S.A, S.a_bytes);
-    const __amdgpu_buffer_rsrc_t rB0 = make_rsrc(S.B0, S.b0_bytes);
-    const __amdgpu_buffer_rsrc_t rB1 = make_rsrc(DUAL ? S.B1 : S.B0, DUAL ? S.b1_bytes : S.b0_bytes);
+    rA = make_rsrc(S.A, S.a_bytes);
+    rB0 = make_rsrc(S.B0, S.b0_bytes);
+    rB1 = make_rsrc(DUAL ? S.B1 : S.B0, DUAL ? S.b1_bytes : S.b0_bytes);
     const int nlo = S.n_lo, nhi = min(S.n_hi, P.N);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      const int row = (4 * i + wave) * 8 + (lane >> 3);
+      const int kc = (lane & 7) ^ swz_key(row);
       const int m = m0 + row;
-      const uint32_t off =
-          m < P.M ? (uint32_t)(((int64_t)m * S.lda + S.a_col + k0 + kc * 8) * 2) : kOob;
-      ra[i] = buf_load16(rA, off);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+      voA[i] = m < P.M ? (uint32_t)(((int64_t)m * S.lda + S.a_col + kc * 8) * 2) : kOob;
       const bool hi = DUAL && i >= 4;  // rows 128..255 of the dual tile
       const int n = n0 + (DUAL ? (row & 127) : row);
       const int64_t ld = hi ? S.ldb1 : S.ldb0;
       const int r0 = hi ? S.b1_row0 : S.b0_row0;
-      const uint32_t off = (n >= nlo && n < nhi) ? (uint32_t)(((int64_t)(n - r0) * ld + k0 + kc * 8) * 2) : kOob;
-      rb[i] = buf_load16(hi ? rB1 : rB0, off);
+      voB[i] = (n >= nlo && n < nhi) ? (uint32_t)(((int64_t)(n - r0) * ld + kc * 8) * 2) : kOob;
     }
   };
-  auto lstore = [&](int buf) {
-    uint16_t* As = smem + buf * 2 * kTileElems;
-    uint16_t* Bs = As + kTileElems;
+  int ls = next_active(P.seg0 - 1), lk = 0;  // next K-step to load
+  int lK = 0;                                 // K of segment ls
+  typedef __attribute__((address_space(3))) void lds_void;
+  auto issue = [&](int stage) {
+    const uint32_t so = (uint32_t)lk * 2;
+    uint16_t* base = smem + stage * kStageElems;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
-      *reinterpret_cast<u32x4*>(As + swz(row, kc)) = ra[i];
-      *reinterpret_cast<u32x4*>(Bs + swz(row, kc)) = rb[i];
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void*)(base + (4 * i + wave) * 8 * kBK), 16, voA[i], so, 0,
+                                               0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds((DUAL && i >= 4) ? rB1 : rB0,
+                                               (lds_void*)(base + kTileElems + (4 * i + wave) * 8 * kBK), 16, voB[i],
+                                               so, 0, 0);
+  };
+  // Moves the load position one K-step on. Past the last segment every
+  // offset becomes kOob: trailing loads deliver zeros without touching
+  // memory, which keeps the per-step load count (and so the vmcnt
+  // arithmetic below) the same in every iteration.
+  auto advance = [&]() {
+    lk += kBK;
+    if (lk >= lK) {
+      ls = next_active(ls);
+      lk = 0;
+      if (ls < send) {
+        setup(ls);
+        lK = args.s[ls].K;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) voA[i] = voB[i] = kOob;
+      }
     }
   };
 
@@ -249,53 +289,88 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  auto compute = [&](int buf) {
-    const uint16_t* As = smem + buf * 2 * kTileElems;
-    const uint16_t* Bs = As + kTileElems;
-    const int lr = lane & 31, lk = lane >> 5;
+  // ---- compute side: a K-step is four substeps of 16; fragments of the
+  // next substep are read from LDS while the 16 MFMAs of the current one run.
+  const int lr = lane & 31, lkh = lane >> 5;
+  int aoff[4], boff[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int kc = ks * 2 + lk;
-      bf16x8 a[4], b[4];
+  for (int i = 0; i < 4; ++i) aoff[i] = (wm * 128 + i * 32 + lr) * kBK;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(As + swz(wm * 128 + i * 32 + lr, kc));
+  for (int j = 0; j < 4; ++j)
+    boff[j] = kTileElems + ((DUAL ? ((j >> 1) * 128 + wn * 64 + (j & 1) * 32) : (wn * 128 + j * 32)) + lr) * kBK;
+  const int sw = swz_key(lr);  // every fragment row this lane reads is lr mod 32
+  bf16x8 fa[2][4], fb[2][4];
+  auto frag = [&](int stage, int ks, int slot) {
+    const uint16_t* base = smem + stage * kStageElems;
+    const int ch = ((ks * 2 + lkh) ^ sw) << 3;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int br = DUAL ? ((j >> 1) * 128 + wn * 64 + (j & 1) * 32) : (wn * 128 + j * 32);
-        b[j] = *reinterpret_cast<const bf16x8*>(Bs + swz(br + lr, kc));
-      }
+    for (int i = 0; i < 4; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8*>(base + aoff[i] + ch);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j) fb[slot][j] = *reinterpret_cast<const bf16x8*>(base + boff[j] + ch);
+  };
+  auto mma = [&](int slot) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
   };
 
-  int s = next_active(P.seg0 - 1);
-  if (s < send) {
-    int k0 = 0;
-    gload(s, k0);
-    lstore(0);
+  // total K-steps over the segments this tile touches
+  int T = 0;
+  for (int s = ls; s < send; s = next_active(s)) T += args.s[s].K / kBK;
+  if (T > 0) {
+    setup(ls);
+    lK = args.s[ls].K;
+    issue(0);  // step 0
+    advance();
+    __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
     __syncthreads();
-    int buf = 0;
-    while (true) {
-      int ns = s, nk = k0 + kBK;
-      if (nk >= args.s[s].K) {
-        ns = next_active(s);
-        nk = 0;
-      }
-      const bool more = ns < send;
-      if (more) gload(ns, nk);
-      compute(buf);
-      if (more) lstore(buf ^ 1);
+    issue(1);  // step 1 (zeros if T == 1)
+    advance();
+    frag(0, 0, 0);
+    // Per K-step `it` (stage st = it&1, other stage ot):
+    //   phases 1-3  MFMAs of substeps 0..2 | fragment reads of substeps 1..3
+    //   wait for this thread's loads of step it+1, barrier: step it+1 is in
+    //               `ot` for everyone and nobody reads `st` any more
+    //   phase 4     MFMAs of substep 3 | loads of step it+2 into `st`,
+    //               fragment reads of substep 0 of step it+1 from `ot`
+    // In the last iteration the loads carry zeros into a stage that is not
+    // read again before the epilogue's barrier.
+    for (int it = 0; it < T; ++it) {
+      const int st = it & 1;
+#define GLT_PHASE(FKS, FSLOT, MSLOT)                                \
+      frag(st, FKS, FSLOT);                                         \
+      mma(MSLOT);                                                   \
+      _Pragma("unroll") for (int q = 0; q < 8; ++q) {               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          \
+      }                                                             \
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);            \
+      __builtin_amdgcn_sched_barrier(0);
+      GLT_PHASE(1, 1, 0)
+      GLT_PHASE(2, 0, 1)
+      GLT_PHASE(3, 1, 0)
+#undef GLT_PHASE
+      __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
       __syncthreads();
-      if (!more) break;
-      s = ns;
-      k0 = nk;
-      buf ^= 1;
+      __builtin_amdgcn_sched_barrier(0);
+      issue(st);
+      frag(st ^ 1, 0, 0);
+      mma(1);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);           // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      advance();
     }
+    // trailing (zero) loads must land before the epilogue reuses LDS
+    __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
+    __syncthreads();
   }
 
   // Epilogue, staged through LDS (the main loop's last barrier released it):
