@@ -86,18 +86,16 @@ def main():
     wu = fill(torch.empty((I, D), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_UP, 0.0, 0.02)
     wd = fill(torch.empty((D, I), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_DOWN, 0.0, 0.02)
     masters = fill(torch.empty(3 * S * D, dtype=torch.float32, device=dev), 1, 1, 0.0, 0.02)
-    packed = torch.empty(6 * S * D, dtype=bf, device=dev)
-    wg_t, wu_t = torch.empty((D, I), dtype=bf, device=dev), torch.empty((D, I), dtype=bf, device=dev)
-    wd_t = torch.empty((I, D), dtype=bf, device=dev)
+    packed = torch.empty(lib.glt_graft_packed_size(S, D), dtype=torch.uint8, device=dev)
 
     sl = (F.GraftSlice * 1)()
     sl[0] = F.GraftSlice(I, S, 0, D, masters.data_ptr(), masters.data_ptr() + 4 * S * D,
                          masters.data_ptr() + 8 * S * D, packed.data_ptr())
     desc = F.MlpDesc(M, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT, 1, sl, None)
-    F.call("glt_base_prepare", ctypes.byref(desc), p(wg), p(wu), p(wd), p(wg_t), p(wu_t), p(wd_t), sp)
+    prepared = torch.empty(lib.glt_base_prepared_size(ctypes.byref(desc)), dtype=torch.uint8, device=dev)
+    F.call("glt_base_prepare", ctypes.byref(desc), p(wg), p(wu), p(wd), p(prepared), sp)
     F.call("glt_graft_pack", sl, p(packed), sp)
-    base = F.BaseWeights(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), wg_t.data_ptr(), wu_t.data_ptr(),
-                         wd_t.data_ptr())
+    base = F.BaseWeights(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), prepared.data_ptr())
 
     x = torch.empty((M, D), dtype=bf, device=dev)
     var = torch.empty(M, dtype=torch.float32, device=dev)

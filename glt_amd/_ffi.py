@@ -43,7 +43,7 @@ class GraftGrads(ctypes.Structure):
 
 
 class BaseWeights(ctypes.Structure):
-    _fields_ = [("gate", _vp), ("up", _vp), ("down", _vp), ("gate_t", _vp), ("up_t", _vp), ("down_t", _vp)]
+    _fields_ = [("gate", _vp), ("up", _vp), ("down", _vp), ("prepared", _vp)]
 
 
 class MlpDesc(ctypes.Structure):
@@ -68,9 +68,11 @@ SIGNATURES = {
     "glt_f32_to_bf16": (_i32, [_vp, _vp, _i64, _vp]),
     "glt_fill_normal": (_i32, [_vp, _i32, _i64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double,
                                ctypes.c_double, _vp]),
+    "glt_graft_packed_size": (_sz, [_i32, _i32]),
     "glt_graft_pack": (_i32, [ctypes.POINTER(GraftSlice), _vp, _vp]),
     "glt_transpose": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp]),
-    "glt_base_prepare": (_i32, [ctypes.POINTER(MlpDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "glt_base_prepared_size": (_sz, [ctypes.POINTER(MlpDesc)]),
+    "glt_base_prepare": (_i32, [ctypes.POINTER(MlpDesc), _vp, _vp, _vp, _vp, _vp]),
     "glt_graft_gemm": (_i32, [_i32, _i32, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _f32, _f32, _vp]),
     "glt_mlp_fwd": (_i32, [ctypes.POINTER(MlpDesc), ctypes.POINTER(BaseWeights), _vp, _vp, _vp, _vp, _vp, _vp]),
     "glt_mlp_bwd_workspace_size": (_sz, [ctypes.POINTER(MlpDesc)]),

@@ -6,6 +6,7 @@ glt_amd/libglt.so next to this file.
 """
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -22,7 +23,11 @@ FLAGS = [
     # packed-f32 VALU forms are kept out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+    # per-kernel register / scratch report, checked below
+    "-Rpass-analysis=kernel-resource-usage",
 ]
+_RE_NAME = re.compile(r"remark: Function Name: (\S+)")
+_RE_SCRATCH = re.compile(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)")
 
 
 def sources():
@@ -35,6 +40,17 @@ def _compile(src):
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+    # No kernel may use scratch: in these kernels it only ever appears as a
+    # register spill or a copied argument block, both silent slowdowns.
+    name = None
+    for line in r.stderr.splitlines():
+        m = _RE_NAME.search(line)
+        if m:
+            name = m.group(1)
+            continue
+        m = _RE_SCRATCH.search(line)
+        if m and int(m.group(1)) > 0:
+            raise RuntimeError(f"{os.path.basename(src)}: kernel {name} uses {m.group(1)} bytes/lane of scratch")
     return obj
 
 

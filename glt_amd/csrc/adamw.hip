@@ -3,10 +3,10 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "layout.hpp"
 
 namespace glt {
 
-glt_status transpose_f32_to_bf16(const float* src, uint16_t* dst, int rows, int cols, hipStream_t st);
 
 constexpr int kClipBlocks = 1024;
 
@@ -120,13 +120,12 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
     for (int p = 0; p < 3; ++p) {
       if (!masters[p] || !(proj_mask & (1 << p))) continue;
       float* w = const_cast<float*>(masters[p]);
-      uint16_t* mirror = packed_out && packed_out[j] ? packed_out[j] + 2 * p * sh : nullptr;
       GLT_LAUNCH("adamw", adamw_kernel, dim3(grid_n(sh)), dim3(256), 0, st, w, grads[j] + p * sh,
-                         m[j] + p * sh, v[j] + p * sh, mirror, sh, lr, beta1, beta2, b1c, b2c, eps,
+                         m[j] + p * sh, v[j] + p * sh, (uint16_t*)nullptr, sh, lr, beta1, beta2, b1c, b2c, eps,
                          weight_decay, (const float*)nullptr, 0, 0.f);
       GLT_LAUNCH_CHECK("adamw_graft");
-      if (mirror) {
-        glt_status s = transpose_f32_to_bf16(w, mirror + sh, sl.s, sl.h, st);
+      if (packed_out && packed_out[j]) {
+        glt_status s = pack_projection(w, sl.s, sl.h, p, packed_out[j], st);
         if (s != GLT_OK) return s;
       }
     }

@@ -3,6 +3,7 @@
 #include <cmath>
 
 #include "gemm.hpp"
+#include "layout.hpp"
 
 namespace glt {
 
@@ -55,20 +56,15 @@ __device__ __forceinline__ void epilogue(const GProb& P, int m, int n, float a0,
   }
 }
 
-// Locates this workgroup's problem and tile. XCD-aware: consecutive
-// workgroup ids are dealt round-robin over the 8 XCDs, so ids are remapped
-// to give each XCD one contiguous range of tiles; within a problem tiles run
-// in groups of kGroupM M-tiles so neighbouring workgroups share A and B rows
-// in that XCD's L2.
+// Locates problem and tile of tile index t. Within a problem tiles run in
+// groups of kGroupM M-tiles, so tiles with neighbouring indices share A and
+// B rows in L2.
 constexpr int kGroupM = 8;
-__device__ __forceinline__ int locate_tile(const GArgs& args, int& tm, int& tn, bool xcd_remap) {
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if (xcd_remap && (nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+__device__ __forceinline__ int locate_tile(const GArgs& args, int t, int& tm, int& tn) {
   int pi = 0;
-  while (pi + 1 < args.nprob && bid >= args.p[pi + 1].tile_begin) ++pi;
+  while (pi + 1 < args.nprob && t >= args.p[pi + 1].tile_begin) ++pi;
   const GProb& P = args.p[pi];
-  const int t = bid - P.tile_begin;
+  t -= P.tile_begin;
   const int per_group = kGroupM * P.tiles_n;
   const int g = t / per_group;
   const int first_m = g * kGroupM;
@@ -86,25 +82,40 @@ __device__ __forceinline__ bool seg_hits(const GSeg& S, const GProb& P, int n0, 
 // =========================================================================
 // gfx950 MFMA kernel: bf16 x bf16 -> f32, v_mfma_f32_32x32x16_bf16.
 //
-// Workgroup tile 256 (M) x 256 B-rows, K in steps of 32, 4 wavefronts in a
+// Workgroup tile 256 (M) x 256 B-rows, K in steps of 64, 4 wavefronts in a
 // 2x2 arrangement; each wavefront owns 128x128 outputs = 4x4 MFMA 32x32
 // tiles (256 fp32 accumulators per lane, in AGPRs). Plain form: the 256
 // B-rows are 256 output columns. Dual form: B-rows [0,128) are gate rows and
 // [128,256) the up rows of the same 128 output columns.
 //
-// Global -> LDS: direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds):
-// each wavefront instruction moves 1 KB (8 rows x 128 bytes) straight into
-// LDS, lane L landing at base + 16*L; rows outside a tile's valid range get
-// an out-of-range offset and arrive as zeros. Two 64 KB stages alternate;
-// the loads of step it+1 are issued as soon as the barrier late in step it-1
-// frees their stage, a full K-step ahead of their use, and no VGPRs or
-// ds_write instructions carry the tiles.
+// Persistent: the grid is one workgroup per CU; workgroup b walks tiles
+// xb, xb + G, xb + 2G, ... (G = grid size). Workgroups are dealt
+// round-robin over the 8 XCDs, so xb = (b & 7) * G/8 + b / 8 gives the 32
+// workgroups of one XCD 32 consecutive tiles per round, which share A and B
+// rows in that XCD's L2.
+//
+// Operands. LDS bandwidth is the scarce resource of this tile shape, so only
+// A (activations, row-major) goes through LDS: direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds), each wavefront instruction moving 1 KB
+// (8 rows x 128 bytes) with lane L landing at base + 16*L, into a ring of
+// four 32 KB stages, issued three K-steps ahead of use. B (weights) is read
+// from the shuffled layout of layout.hpp straight into registers: per
+// K-substep a wavefront's four 32-row fragments are four coalesced 1 KB
+// loads, issued one K-step ahead. Rows outside a tile's valid range get an
+// out-of-range offset and arrive as zeros. The load side walks the K-steps
+// of all of the workgroup's tiles as one stream, so the next tile's first
+// steps are in flight while the epilogue of the current one runs; the
+// epilogue stages accumulators through a separate 32 KB area, private per
+// wavefront.
 // =========================================================================
 constexpr int kBM = 256, kBK = 64;
-constexpr int kStages = 2;
-constexpr int kTileElems = kBM * kBK;                    // one operand tile
-constexpr int kStageElems = 2 * kTileElems;              // A then B
-constexpr size_t kMfmaLds = (size_t)kStages * kStageElems * 2;  // 128 KB
+constexpr int kTileElems = kBM * kBK;                    // one A tile = one LDS stage (32 KB)
+constexpr int kAStages = 4;
+constexpr uint32_t kExtent = 0x7FFFFFF0u;                // buffer extent below kOob
+constexpr int kEpRows = 16;                              // rows per staged half-band
+constexpr int kEpWaveWords = kEpRows * 128;              // f32 staging words per wavefront
+constexpr size_t kMfmaLds = ((size_t)kAStages * kTileElems * 2) + 4 * kEpWaveWords * 4;  // 160 KB
+constexpr uint32_t kShufStepBytes = kShufBlock * 2;      // one 32 x 64 block of B (4 KB)
 
 // Rows are 64 bf16 = 128 bytes, one cache line each, so every global
 // request a tile issues moves a whole line. gfx950 LDS serves a
@@ -114,11 +125,38 @@ constexpr size_t kMfmaLds = (size_t)kStages * kStageElems * 2;  // 128 KB
 // logical one XOR (row>>1)&7, which makes the 16 groups distinct.
 __device__ __forceinline__ int swz_key(int row) { return (row >> 1) & 7; }
 
+// Epilogue staging layout: row-major 16 x 128 f32 per wavefront, column
+// XOR-swizzled so that (a) the accumulator writes, where lanes 0-31 and
+// 32-63 fill rows four apart, hit all 64 banks (bit 5 follows row bit 2) and
+// (b) the 16-byte row reads of 16 lanes, which cover 128 columns, split over
+// both bank halves (bit 2 follows column bit 6 and row bit 0).
+__device__ __forceinline__ int ep_col(int row, int col) {
+  return col ^ (((row >> 2) & 1) << 5) ^ ((((col >> 6) ^ row) & 1) << 2);
+}
+
+// Buffer descriptor of a wave-uniform base and extent. The compiler loses
+// track of their uniformity through the kernel's position bookkeeping and
+// would wrap every buffer load in a per-lane loop over descriptor values;
+// readfirstlane states it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uni_rsrc(const void* p, uint32_t n) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(n));
+}
+
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n and leaves
 // expcnt / lgkmcnt unconstrained.
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-constexpr int kEpPitch = 132;  // f32 words per staged epilogue row (128 + pad)
+// Orders one wavefront's LDS accesses across lanes: LDS executes a
+// wavefront's instructions in order, so only the compiler must not move
+// accesses across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 __device__ __forceinline__ void unpack8(const u32x4& q, float* f) {
   f[0] = bf16_to_f32((uint16_t)(q.x & 0xFFFF)); f[1] = bf16_to_f32((uint16_t)(q.x >> 16));
@@ -154,13 +192,17 @@ __device__ __forceinline__ void st8(void* p, int64_t o, const float* f) {
 }
 
 // Eight consecutive output columns n..n+7 of row m (v = accumulators; u =
-// up accumulators in the dual form). Vector path when the chunk is whole;
-// outputs and aux rows are 16-byte aligned (checked on the host).
+// up accumulators in the dual form; gq/uq = the saved bf16 gate/up
+// pre-activations of these columns for EPI_DGDU, loaded ahead). Vector path
+// when the chunk is whole; outputs and aux rows are 16-byte aligned
+// (checked on the host).
 template <typename TO, int MODE>
-__device__ __forceinline__ void epi_chunk(const GProb& P, int m, int n, const float* v, const float* u) {
+__device__ __forceinline__ void epi_chunk(const GProb& P, int m, int n, const float* v, const float* u,
+                                          const u32x4& gq, const u32x4& uq) {
   if (m >= P.M) return;
   if (n + 8 > P.N) {
-    for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)  // unrolled: v and u live in registers
       if (n + j < P.N) epilogue<TO, MODE>(P, m, n + j, v[j], u[j]);
     return;
   }
@@ -185,10 +227,10 @@ __device__ __forceinline__ void epi_chunk(const GProb& P, int m, int n, const fl
     if (P.out1) st8<TO>(P.out1, o, g);
     if (P.out2) st8<TO>(P.out2, o, uu);
   } else {
+    static_assert(MODE != EPI_DGDU || sizeof(TO) == 2, "the staged DGDU epilogue reads bf16 aux");
     float g[8], uu[8], du[8];
-    const int64_t oa = (int64_t)m * P.ldaux + n;
-    ld8<TO>(P.aux0, oa, g);
-    ld8<TO>(P.aux1, oa, uu);
+    unpack8(gq, g);
+    unpack8(uq, uu);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float sg = 1.0f / (1.0f + expf(-g[j]));
@@ -209,214 +251,335 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  int tm, tn;
-  const int pi = locate_tile(args, tm, tn, true);
-  const GProb& P = args.p[pi];
-  const int m0 = tm * kBM, n0 = tn * BN;
-  const int send = P.seg0 + P.nseg;
+  const int G = gridDim.x, total = args.total_tiles;
+  const int b = blockIdx.x;
+  const int first = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
 
-  auto next_active = [&](int s) {
+  auto next_active = [&](const GProb& P, int n0, int s, int send) {
     ++s;
     while (s < send && !seg_hits(args.s[s], P, n0, BN)) ++s;
     return s;
   };
 
-  // ---- load side. Per K-step each wavefront issues 8 A and 8 B
-  // direct-to-LDS loads: instruction i of wave w fills tile rows
-  // 8*g .. 8*g+7 with g = 4*i + w; lane L takes row 8*g + L/8 and physical
-  // chunk L&7, i.e. logical chunk (L&7) ^ swz_key(row). Buffer descriptors
-  // and per-lane byte offsets are set once per segment; the K position rides
-  // in the scalar offset.
-  __amdgpu_buffer_rsrc_t rA, rB0, rB1;
-  uint32_t voA[8], voB[8];
-  auto setup = [&](int s) {
-    const GSeg& S = args.s[s];
-    rA = make_rsrc(S.A, S.a_bytes);
-    rB0 = make_rsrc(S.B0, S.b0_bytes);
-    rB1 = make_rsrc(DUAL ? S.B1 : S.B0, DUAL ? S.b1_bytes : S.b0_bytes);
-    const int nlo = S.n_lo, nhi = min(S.n_hi, P.N);
+  // ---- K-step stream positions: tile t, its problem pi, origin (m0, n0),
+  // segment s (of [seg0, send)), K offset k within the segment's K.
+  struct Pos {
+    int t, pi, m0, n0, send, s, k, K;
+  };
+  // Moves q to the first active segment of tile q.t or of a later tile of
+  // this workgroup (tiles without one have no K-steps); false past the end.
+  auto first_seg = [&](Pos& q) {
+    for (; q.t < total; q.t += G) {
+      int tm, tn;
+      q.pi = locate_tile(args, q.t, tm, tn);
+      const GProb& P = args.p[q.pi];
+      q.m0 = tm * kBM;
+      q.n0 = tn * BN;
+      q.send = P.seg0 + P.nseg;
+      q.s = next_active(P, q.n0, P.seg0 - 1, q.send);
+      if (q.s < q.send) {
+        q.k = 0;
+        q.K = args.s[q.s].K;
+        return true;
+      }
+    }
+    return false;
+  };
+  // One K-step on: 0 = same segment, 1 = a new segment, 2 = past the end.
+  auto step_pos = [&](Pos& q) {
+    if (q.t >= total) return 2;
+    q.k += kBK;
+    if (q.k < q.K) return 0;
+    q.k = 0;
+    q.s = next_active(args.p[q.pi], q.n0, q.s, q.send);
+    if (q.s < q.send) {
+      q.K = args.s[q.s].K;
+      return 1;
+    }
+    q.t += G;
+    return first_seg(q) ? 1 : 2;
+  };
+
+  // ---- A side: 8 direct-to-LDS loads per wavefront per K-step; load i of
+  // wave w fills tile rows 8*g .. 8*g+7 with g = 4*i + w; lane L takes row
+  // 8*g + L/8 and physical chunk L&7, i.e. logical chunk (L&7) ^
+  // swz_key(row). Past the end of the stream every offset is kOob: trailing
+  // loads deliver zeros without touching memory, which keeps the per-step
+  // load count (and so the vmcnt arithmetic below) the same in every step.
+  Pos pa{first, 0, 0, 0, 0, 0, 0, 0};
+  const void* pA = nullptr;
+  uint32_t nA = 0, voA[8];
+  auto setup_a = [&]() {
+    const GSeg& S = args.s[pa.s];
+    const GProb& P = args.p[pa.pi];
+    pA = S.A;
+    nA = pA ? kExtent : 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int row = (4 * i + wave) * 8 + (lane >> 3);
       const int kc = (lane & 7) ^ swz_key(row);
-      const int m = m0 + row;
+      const int m = pa.m0 + row;
       voA[i] = m < P.M ? (uint32_t)(((int64_t)m * S.lda + S.a_col + kc * 8) * 2) : kOob;
-      const bool hi = DUAL && i >= 4;  // rows 128..255 of the dual tile
-      const int n = n0 + (DUAL ? (row & 127) : row);
-      const int64_t ld = hi ? S.ldb1 : S.ldb0;
-      const int r0 = hi ? S.b1_row0 : S.b0_row0;
-      voB[i] = (n >= nlo && n < nhi) ? (uint32_t)(((int64_t)(n - r0) * ld + kc * 8) * 2) : kOob;
     }
   };
-  int ls = next_active(P.seg0 - 1), lk = 0;  // next K-step to load
-  int lK = 0;                                 // K of segment ls
+  auto end_a = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) voA[i] = kOob;
+  };
+  auto adv_a = [&]() {
+    const int r = step_pos(pa);
+    if (r == 1) setup_a();
+    else if (r == 2) end_a();
+  };
   typedef __attribute__((address_space(3))) void lds_void;
-  auto issue = [&](int stage) {
-    const uint32_t so = (uint32_t)lk * 2;
-    uint16_t* base = smem + stage * kStageElems;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void*)(base + (4 * i + wave) * 8 * kBK), 16, voA[i], so, 0,
-                                               0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds((DUAL && i >= 4) ? rB1 : rB0,
-                                               (lds_void*)(base + kTileElems + (4 * i + wave) * 8 * kBK), 16, voB[i],
-                                               so, 0, 0);
-  };
-  // Moves the load position one K-step on. Past the last segment every
-  // offset becomes kOob: trailing loads deliver zeros without touching
-  // memory, which keeps the per-step load count (and so the vmcnt
-  // arithmetic below) the same in every iteration.
-  auto advance = [&]() {
-    lk += kBK;
-    if (lk >= lK) {
-      ls = next_active(ls);
-      lk = 0;
-      if (ls < send) {
-        setup(ls);
-        lK = args.s[ls].K;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) voA[i] = voB[i] = kOob;
-      }
-    }
+  auto load_a = [&](int stage, int i) {
+    uint16_t* dst = smem + stage * kTileElems + (4 * i + wave) * 8 * kBK;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(uni_rsrc(pA, nA), (lds_void*)dst, 16, voA[i], (uint32_t)pa.k * 2, 0, 0);
   };
 
+  // ---- B side: fragment j of this wavefront covers B rows
+  // n0 + (dual: wn*64 + (j&1)*32, from B1 for j >= 2; plain: wn*128 + j*32)
+  // .. +31. Its per-lane offset selects the 32-row block and the lane's
+  // 16 bytes in it; the K-step and substep ride in the scalar offset.
+  Pos pb{first, 0, 0, 0, 0, 0, 0, 0};
+  const void *pB0 = nullptr, *pB1 = nullptr;
+  uint32_t nB0 = 0, nB1 = 0, voB[4];
+  auto setup_b = [&]() {
+    const GSeg& S = args.s[pb.s];
+    const GProb& P = args.p[pb.pi];
+    pB0 = S.B0;
+    pB1 = DUAL ? S.B1 : S.B0;
+    nB0 = pB0 ? kExtent : 0;
+    nB1 = pB1 ? kExtent : 0;
+    const int nlo = S.n_lo, nhi = min(S.n_hi, P.N);
+    auto voff = [&](int j, int64_t ld, int r0) {
+      const int f0 = pb.n0 + (DUAL ? wn * 64 + (j & 1) * 32 : wn * 128 + j * 32);
+      const int n = f0 + (lane & 31);
+      return (n >= nlo && n < nhi) ? (uint32_t)((int64_t)((f0 - r0) >> 5) * ld * 64 + lane * 16) : kOob;
+    };
+    // Separate loops for the two operands: a per-fragment choice between
+    // two fields of the argument block makes the compiler copy the block to
+    // scratch.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) voB[j] = voff(j, S.ldb0, S.b0_row0);
+#pragma unroll
+    for (int j = 2; j < 4; ++j) voB[j] = DUAL ? voff(j, S.ldb1, S.b1_row0) : voff(j, S.ldb0, S.b0_row0);
+  };
+  auto end_b = [&]() {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) voB[j] = kOob;
+  };
+  auto adv_b = [&]() {
+    const int r = step_pos(pb);
+    if (r == 1) setup_b();
+    else if (r == 2) end_b();
+  };
+  bf16x8 fb[4][4];  // [substep][fragment]
+  auto load_b = [&](int s, int j) {
+    const __amdgpu_buffer_rsrc_t r = (DUAL && j >= 2) ? uni_rsrc(pB1, nB1) : uni_rsrc(pB0, nB0);
+    const uint32_t so = (uint32_t)(pb.k / kBK) * kShufStepBytes + s * 1024;
+    fb[s][j] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voB[j], so, 0));
+  };
+
+  // ---- compute side. A K-step is four substeps of 16; the A fragments of
+  // the next substep are read from LDS while the 16 MFMAs of the current
+  // one run, and each B fragment is reloaded for the next K-step as soon as
+  // its four MFMAs have been issued.
   f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-  // ---- compute side: a K-step is four substeps of 16; fragments of the
-  // next substep are read from LDS while the 16 MFMAs of the current one run.
   const int lr = lane & 31, lkh = lane >> 5;
-  int aoff[4], boff[4];
+  int aoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) aoff[i] = (wm * 128 + i * 32 + lr) * kBK;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    boff[j] = kTileElems + ((DUAL ? ((j >> 1) * 128 + wn * 64 + (j & 1) * 32) : (wn * 128 + j * 32)) + lr) * kBK;
   const int sw = swz_key(lr);  // every fragment row this lane reads is lr mod 32
-  bf16x8 fa[2][4], fb[2][4];
-  auto frag = [&](int stage, int ks, int slot) {
-    const uint16_t* base = smem + stage * kStageElems;
+  bf16x8 fa[2][4];
+  auto read_a = [&](int stage, int ks, int slot, int i) {
     const int ch = ((ks * 2 + lkh) ^ sw) << 3;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8*>(base + aoff[i] + ch);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) fb[slot][j] = *reinterpret_cast<const bf16x8*>(base + boff[j] + ch);
+    fa[slot][i] = *reinterpret_cast<const bf16x8*>(smem + stage * kTileElems + aoff[i] + ch);
   };
-  auto mma = [&](int slot) {
+  // MFMAs of substep s (A slot fs) in four groups, one per B fragment j:
+  // four MFMAs, then the A read i = j of (rst, rks) into slot fs^1, then the
+  // reload of fb[s][j]; `extra` adds work per group (the phase-3 A loads).
+  // The B loads are unconditional: the compiler's waits on fb then stay
+  // one K-step deep.
+  auto phase = [&](int fs, int s, int rst, int rks, auto&& extra) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[fs][i], fb[s][j], acc[i][j], 0, 0, 0);
+      read_a(rst, rks, fs ^ 1, j);
+      load_b(s, j);
+      extra(j);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto no_extra = [](int) {};
+
+  // Pipeline fill: A tiles of K-steps 0..3 into stages 0..3, B of step 0.
+  first_seg(pa);
+  pb = pa;
+  if (pa.t < total) {
+    setup_a();
+    setup_b();
+  } else {
+    end_a();
+    end_b();
+  }
+#pragma unroll 1
+  for (int st = 0; st < kAStages; ++st) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load_a(st, i);
+    adv_a();
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_b(s, j);
+  adv_b();
+  // A of step 0: issued first, followed by 24 more A loads and 16 B loads
+  __builtin_amdgcn_s_waitcnt(vmcnt_enc(40));
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) read_a(0, 0, 0, i);
+  int g = 0;  // K-steps consumed so far; step g's A tile sits in stage g % 4
+
+  float* ep = reinterpret_cast<float*>(smem + kAStages * kTileElems) + wave * kEpWaveWords;
+  const int cr = 4 * (lane >> 5), cc = lane & 31;
+  for (int ct = first; ct < total; ct += G) {
+    int tm, tn;
+    const int pi = locate_tile(args, ct, tm, tn);
+    const GProb& P = args.p[pi];
+    const int m0 = tm * kBM, n0 = tn * BN, send = P.seg0 + P.nseg;
+    int T = 0;  // K-steps of this tile over the segments it touches
+    for (int s = next_active(P, n0, P.seg0 - 1, send); s < send; s = next_active(P, n0, s, send))
+      T += args.s[s].K / kBK;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
-  };
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  // total K-steps over the segments this tile touches
-  int T = 0;
-  for (int s = ls; s < send; s = next_active(s)) T += args.s[s].K / kBK;
-  if (T > 0) {
-    setup(ls);
-    lK = args.s[ls].K;
-    issue(0);  // step 0
-    advance();
-    __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
-    __syncthreads();
-    issue(1);  // step 1 (zeros if T == 1)
-    advance();
-    frag(0, 0, 0);
-    // Per K-step `it` (stage st = it&1, other stage ot):
-    //   phases 1-3  MFMAs of substeps 0..2 | fragment reads of substeps 1..3
-    //   wait for this thread's loads of step it+1, barrier: step it+1 is in
-    //               `ot` for everyone and nobody reads `st` any more
-    //   phase 4     MFMAs of substep 3 | loads of step it+2 into `st`,
-    //               fragment reads of substep 0 of step it+1 from `ot`
-    // In the last iteration the loads carry zeros into a stage that is not
-    // read again before the epilogue's barrier.
-    for (int it = 0; it < T; ++it) {
-      const int st = it & 1;
-#define GLT_PHASE(FKS, FSLOT, MSLOT)                                \
-      frag(st, FKS, FSLOT);                                         \
-      mma(MSLOT);                                                   \
-      _Pragma("unroll") for (int q = 0; q < 8; ++q) {               \
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          \
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          \
-      }                                                             \
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);            \
-      __builtin_amdgcn_sched_barrier(0);
-      GLT_PHASE(1, 1, 0)
-      GLT_PHASE(2, 0, 1)
-      GLT_PHASE(3, 1, 0)
-#undef GLT_PHASE
-      __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
+    // Per K-step g (A stage st = g % 4):
+    //   phases 0-2  MFMAs of substeps 0..2 | A reads of substeps 1..3 |
+    //               B loads of substeps 0..2 of step g+1
+    //   wait for this thread's A loads of step g+1, barrier: step g+1 is in
+    //               LDS for everyone and nobody reads stage st any more
+    //   phase 3     MFMAs of substep 3 | A loads of step g+4 into st |
+    //               A reads of substep 0 of step g+1 | B loads of substep 3
+    // Step g+1 may belong to the next tile: its substep-0 A fragments and
+    // its B fragments stay in registers across the epilogue.
+    for (int it = 0; it < T; ++it, ++g) {
+      const int st = g & (kAStages - 1), nst = (g + 1) & (kAStages - 1);
+      phase(0, 0, st, 1, no_extra);
+      phase(1, 1, st, 2, no_extra);
+      phase(0, 2, st, 3, no_extra);
+      // Loads issued after this thread's A loads of step g+1 (the A loads
+      // of steps g+2, g+3 and the B loads in between): 44 in step 0 and 60
+      // in step 1 (the fill order), at least 64 later. Loads complete in
+      // order, so vmcnt <= n with n at most that count means step g+1 has
+      // landed. (Epilogue stores in between may complete in any order; they
+      // only raise the count.)
+      if (g >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(63));
+      else if (g == 1) __builtin_amdgcn_s_waitcnt(vmcnt_enc(60));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_enc(44));
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
-      issue(st);
-      frag(st ^ 1, 0, 0);
-      mma(1);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);           // VMEM read
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // DS read
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      advance();
+      phase(1, 3, nst, 0, [&](int j) {
+        load_a(st, 2 * j);
+        load_a(st, 2 * j + 1);
+      });
+      adv_a();
+      adv_b();
     }
-    // trailing (zero) loads must land before the epilogue reuses LDS
-    __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
-    __syncthreads();
-  }
 
-  // Epilogue, staged through LDS (the main loop's last barrier released it):
-  // per 32-row band each wavefront writes its accumulators into a private
-  // 32 x 128 f32 block, then reads it back row-wise so every lane handles 8
-  // consecutive columns with 16-byte loads/stores.
-  // 32x32 accumulator layout: lane holds column (lane & 31), rows
-  // 8*(e/4) + 4*(lane/32) + (e%4) for e = 0..15.
-  float* ep = reinterpret_cast<float*>(smem) + wave * (32 * kEpPitch);
-  const int cr = 4 * (lane >> 5), cc = lane & 31;
-  auto stage = [&](const f32x16* a) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) ep[(8 * (e >> 2) + cr + (e & 3)) * kEpPitch + j * 32 + cc] = a[j][e];
-  };
-  // The band loop stays rolled (the chunk code is large); the switch keeps
-  // every accumulator access compile-time indexed, i.e. in registers.
-#pragma unroll 1
-  for (int i = 0; i < 4; ++i) {
-    switch (i) {
-      case 0: stage(acc[0]); break;
-      case 1: stage(acc[1]); break;
-      case 2: stage(acc[2]); break;
-      default: stage(acc[3]); break;
-    }
-    __syncthreads();
-    const int row0 = m0 + wm * 128 + i * 32;
-    if constexpr (DUAL) {
-      // columns [0,64) of the block hold gate, [64,128) up, same output columns
+    // ---- epilogue, per 16-row half-band: accumulators -> private LDS
+    // block -> row-wise reads so every lane handles 8 consecutive columns
+    // with 16-byte loads/stores. A tile without K-steps has zero
+    // accumulators and skips the staging.
+    const int rbase = m0 + wm * 128;
+    __amdgpu_buffer_rsrc_t rG, rU;
+    u32x4 gq[2][4], uq[2][4];
+    auto prefetch = [&](int i, int hh) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = (lane >> 3) + 8 * q, c8 = (lane & 7) * 8;
-        const float* src = ep + r * kEpPitch + c8;
-        epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 64 + c8, src, src + 64);
+        const int m = rbase + i * 32 + hh * 16 + (lane >> 4) + 4 * q;
+        const int n = n0 + wn * 128 + (lane & 15) * 8;
+        const uint32_t off = (m < P.M && n + 8 <= P.N) ? (uint32_t)(((int64_t)m * P.ldaux + n) * 2) : kOob;
+        gq[hh][q] = buf_load16(rG, off);
+        uq[hh][q] = buf_load16(rU, off);
       }
-    } else {
+    };
+    if constexpr (MODE == EPI_DGDU) {
+      rG = make_rsrc(P.aux0, kExtent);
+      rU = make_rsrc(P.aux1, kExtent);
+    }
+    auto stage_half = [&](const f32x16* a, int e0) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int r = (lane >> 4) + 4 * q, c8 = (lane & 15) * 8;
-        const float* src = ep + r * kEpPitch + c8;
-        epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 128 + c8, src, src);
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int row = 8 * (e >> 2) + cr + (e & 3);
+          ep[row * 128 + ep_col(row, j * 32 + cc)] = a[j][e0 + e];
+        }
+    };
+    auto read8 = [&](int row, int col, float* v) {
+      if (T == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.f;
+        return;
+      }
+      const float* p = ep + row * 128;
+      const int c0 = ep_col(row, col);
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(p + c0);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(p + (c0 ^ 4));
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w; v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+    };
+    // The band loop stays rolled (the chunk code is large); the switch keeps
+    // every accumulator access compile-time indexed, i.e. in registers.
+#pragma unroll 1
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        // this half-band's aux rows, in flight while its accumulators are
+        // staged (a look-ahead would need more registers than remain)
+        if constexpr (MODE == EPI_DGDU) prefetch(i, hh);
+        if (T > 0) {
+          switch (i) {
+            case 0: stage_half(acc[0], hh * 8); break;
+            case 1: stage_half(acc[1], hh * 8); break;
+            case 2: stage_half(acc[2], hh * 8); break;
+            default: stage_half(acc[3], hh * 8); break;
+          }
+        }
+        wave_lds_sync();
+        const int row0 = rbase + i * 32 + hh * 16;
+        if constexpr (DUAL) {
+          // columns [0,64) of the block hold gate, [64,128) up, same output columns
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const int r = (lane >> 3) + 8 * q, c8 = (lane & 7) * 8;
+            float v[8], u[8];
+            read8(r, c8, v);
+            read8(r, 64 + c8, u);
+            epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 64 + c8, v, u, gq[0][0], uq[0][0]);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int r = (lane >> 4) + 4 * q, c8 = (lane & 15) * 8;
+            float v[8];
+            read8(r, c8, v);
+            epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 128 + c8, v, v, gq[hh][q], uq[hh][q]);
+            // one chunk at a time: overlapping them costs registers the
+            // aux prefetch needs
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        wave_lds_sync();
       }
     }
-    __syncthreads();
   }
+  // trailing (zero) loads must land before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
 }
 
 // =========================================================================
@@ -437,7 +600,7 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(const GArgs args) {
   __shared__ float Bs[NB][BK][BN + 1];
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   int tm, tn;
-  const int pi = locate_tile(args, tm, tn, false);
+  const int pi = locate_tile(args, blockIdx.x, tm, tn);
   const GProb& P = args.p[pi];
   const int m0 = tm * BM, n0 = tn * BN;
   float acc[NB][4][4] = {};
@@ -491,19 +654,21 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(const GArgs args) {
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 bool gemm_mfma_eligible(const GemmPlan& plan) {
-  if (plan.a_kind != LD_BF16 || plan.b_kind != LD_BF16) return false;
+  if (plan.a_kind != LD_BF16 || plan.b_kind != LD_SHUF) return false;
   for (int i = 0; i < plan.nseg; ++i) {
     const GSeg& s = plan.args.s[i];
-    if (s.a_ks != 1 || s.b_ks != 1) return false;
-    if (s.K % kBK != 0 || s.a_col % 8 != 0 || s.lda % 8 != 0 || s.ldb0 % 8 != 0) return false;
-    if (!al16(s.A) || !al16(s.B0)) return false;
-    if (plan.dual && (s.ldb1 % 8 != 0 || !al16(s.B1))) return false;
+    if (s.a_ks != 1 || s.K % kBK != 0 || s.a_col % 8 != 0 || s.lda % 8 != 0 || !al16(s.A)) return false;
+    // B fragments start on 32-row blocks of the shuffled operand
+    if (s.n_lo % 32 != 0 || s.b0_row0 % 32 != 0 || s.ldb0 % kBK != 0 || s.K > s.ldb0 || !al16(s.B0)) return false;
+    if (plan.dual && (s.b1_row0 % 32 != 0 || s.ldb1 % kBK != 0 || s.K > s.ldb1 || !al16(s.B1))) return false;
   }
   for (int p = 0; p < plan.args.nprob; ++p) {
     const GProb& P = plan.args.p[p];
     // the staged epilogue stores 8-column chunks with 16-byte accesses
     if (P.ldo % 8 || !al16(P.out0) || !al16(P.out1) || !al16(P.out2)) return false;
     if (P.mode == EPI_DGDU && (P.ldaux % 8 || !al16(P.aux0) || !al16(P.aux1))) return false;
+    // the DGDU epilogue reads aux rows through 31-bit buffer offsets
+    if (P.mode == EPI_DGDU && (int64_t)(P.M + kBM) * P.ldaux * 2 >= (int64_t)kOob) return false;
     for (int i = P.seg0; i < P.seg0 + P.nseg; ++i) {
       const GSeg& s = plan.args.s[i];
       // every byte offset a tile forms must fit the 31-bit buffer range
@@ -515,6 +680,20 @@ bool gemm_mfma_eligible(const GemmPlan& plan) {
   return true;
 }
 
+// CUs of the current device (the persistent grid size), cached per device.
+static glt_status device_cus(int& cus) {
+  static int cached[64] = {};
+  int dev = 0;
+  GLT_TRY_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) {
+    set_error("gemm: device index %d out of range", dev);
+    return GLT_ERR_HIP;
+  }
+  if (cached[dev] == 0) GLT_TRY_HIP(hipDeviceGetAttribute(&cached[dev], hipDeviceAttributeMultiprocessorCount, dev));
+  cus = cached[dev];
+  return GLT_OK;
+}
+
 template <typename TO, int MODE, bool DUAL>
 static glt_status launch_mfma(const GArgs& a, hipStream_t st, const char* label) {
   static bool attr_set = false;
@@ -524,7 +703,12 @@ static glt_status launch_mfma(const GArgs& a, hipStream_t st, const char* label)
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLds));
     attr_set = true;
   }
-  GLT_LAUNCH(label, fn, dim3(a.total_tiles), dim3(256), kMfmaLds, st, a);
+  int cus = 0;
+  const glt_status rc = device_cus(cus);
+  if (rc != GLT_OK) return rc;
+  // one workgroup per CU (160 KB of LDS admits no second one)
+  const int grid = a.total_tiles < cus ? a.total_tiles : cus;
+  GLT_LAUNCH(label, fn, dim3(grid), dim3(256), kMfmaLds, st, a);
   GLT_LAUNCH_CHECK("gemm_mfma");
   return GLT_OK;
 }
@@ -555,15 +739,6 @@ glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma) {
   }
   a.total_tiles = tiles;
   if (tiles == 0) return GLT_OK;
-  // Rows outside a tile's valid range are steered to kOob explicitly and
-  // every in-range offset fits 31 bits (checked above), so the extent only
-  // has to exclude kOob; a missing operand gets extent 0 and reads as zero.
-  for (int i = 0; i < plan.nseg; ++i) {
-    GSeg& s = a.s[i];
-    s.a_bytes = s.A ? 0x7FFFFFF0u : 0;
-    s.b0_bytes = s.B0 ? 0x7FFFFFF0u : 0;
-    s.b1_bytes = s.B1 ? 0x7FFFFFF0u : 0;
-  }
   if (mfma) {
     if (mode == EPI_SILU && plan.dual) return launch_mfma<uint16_t, EPI_SILU, true>(a, st, plan.label);
     if (mode == EPI_DGDU && !plan.dual) return launch_mfma<uint16_t, EPI_DGDU, false>(a, st, plan.label);
@@ -574,6 +749,8 @@ glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma) {
     return GLT_ERR_UNSUPPORTED;
   }
   const int la = plan.a_kind, lb = plan.b_kind;
+  GLT_CHECK(lb != LD_SHUF && la != LD_SHUF, GLT_ERR_UNSUPPORTED,
+            "run_gemm(%s): shuffled operand on a shape the MFMA kernel does not take", plan.label);
 #define GLT_GEN(LA_, LB_, TO_, MODE_, DUAL_)                                                     \
   if (la == LA_ && lb == LB_ && (sizeof(TO_) == 4) == (of32 != 0) && mode == MODE_ && plan.dual == DUAL_) \
     return launch_generic<LA_, LB_, TO_, MODE_, DUAL_>(a, st, plan.label);

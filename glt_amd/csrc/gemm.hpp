@@ -25,17 +25,17 @@ enum EpiMode : int {
   EPI_DGDU = 2,   // out0 = acc*u*silu'(g), out1 = acc*silu(g); g = aux0, u = aux1
 };
 
-// Element kinds a strided operand can be read as.
-enum LoadKind : int { LD_BF16 = 0, LD_F32 = 1, LD_F32_AS_BF16 = 2 };
+// Element kinds an operand can be read as. LD_SHUF: bf16 B operand in the
+// shuffled layout of layout.hpp (MFMA kernel only).
+enum LoadKind : int { LD_BF16 = 0, LD_F32 = 1, LD_F32_AS_BF16 = 2, LD_SHUF = 3 };
 
 struct GSeg {
   const void* A;
   const void* B0;   // single / gate operand
   const void* B1;   // up operand (dual only)
   int64_t lda, a_ks;         // A(m, k) = A[m*lda + k*a_ks]
-  int64_t ldb0, ldb1, b_ks;  // B(n, k) = B[n*ldb + k*b_ks]
+  int64_t ldb0, ldb1, b_ks;  // strided: B(n, k) = B[n*ldb + k*b_ks]; LD_SHUF: ldb = padded K of B
   int a_col, K, n_lo, n_hi, b0_row0, b1_row0;
-  uint32_t a_bytes, b0_bytes, b1_bytes;  // buffer extents (MFMA path)
 };
 
 struct GProb {
@@ -78,9 +78,11 @@ struct GemmPlan {
   }
 };
 
-// Runs the plan: the gfx950 MFMA kernel when every operand is bf16, NT,
-// 16-byte aligned and every K is a multiple of 64; otherwise the strided
-// generic kernel (f32 path, tiny/unaligned shapes, transposed probes).
+// Runs the plan: the gfx950 MFMA kernel when A is bf16 row-major (16-byte
+// aligned rows), B is shuffled (LD_SHUF, 32-aligned row ranges) and every K
+// is a multiple of 64; otherwise the strided generic kernel (f32 path,
+// tiny/unaligned shapes, transposed probes). A shuffled B has no generic
+// form: such a plan must be MFMA-eligible.
 glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma = true);
 bool gemm_mfma_eligible(const GemmPlan& plan);
 

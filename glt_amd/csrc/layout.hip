@@ -1,0 +1,71 @@
+// Shuffled B layout writer (see layout.hpp).
+#include "layout.hpp"
+
+namespace glt {
+
+template <typename TS>
+__device__ __forceinline__ float ld_src(const TS* p, int64_t i) {
+  if constexpr (sizeof(TS) == 4) return p[i];
+  else return bf16_to_f32(p[i]);
+}
+
+// One workgroup per 32 x 64 block: the source tile goes through LDS (read
+// coalesced along the source's contiguous axis), then every thread writes
+// one 16-byte (substep, lane) chunk of the block.
+template <typename TS, bool TR>
+__global__ void __launch_bounds__(256) shuffle_kernel(const TS* __restrict__ src, int64_t ld, int rows, int K,
+                                                      int kblocks, uint16_t* __restrict__ dst) {
+  __shared__ float tile[kShufRows][kShufK + 1];
+  const int blk = blockIdx.x;
+  const int rb = blk / kblocks, kb = blk - rb * kblocks;
+  const int r0 = rb * kShufRows, k0 = kb * kShufK;
+  const int t = threadIdx.x;
+  if constexpr (!TR) {
+    const int r = t >> 3, kc = (t & 7) * 8;  // 32 rows x 8 chunks of 8 along K
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k = k0 + kc + e;
+      tile[r][kc + e] = (r0 + r < rows && k < K) ? ld_src(src, (int64_t)(r0 + r) * ld + k) : 0.f;
+    }
+  } else {
+    const int kk = t >> 2, rc = (t & 3) * 8;  // 64 source rows (K) x 4 chunks of 8 along the rows of B
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int r = r0 + rc + e, k = k0 + kk;
+      tile[rc + e][kk] = (r < rows && k < K) ? ld_src(src, (int64_t)k * ld + r) : 0.f;
+    }
+  }
+  __syncthreads();
+  const int s = t >> 6, lane = t & 63;
+  const int rr = lane & 31, kq = 16 * s + 8 * (lane >> 5);
+  u32x4 q;
+  q.x = pack_bf16x2(tile[rr][kq + 0], tile[rr][kq + 1]);
+  q.y = pack_bf16x2(tile[rr][kq + 2], tile[rr][kq + 3]);
+  q.z = pack_bf16x2(tile[rr][kq + 4], tile[rr][kq + 5]);
+  q.w = pack_bf16x2(tile[rr][kq + 6], tile[rr][kq + 7]);
+  *reinterpret_cast<u32x4*>(dst + (int64_t)blk * kShufBlock + t * 8) = q;
+}
+
+glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed, int rows, int K, uint16_t* dst,
+                     hipStream_t st) {
+  GLT_CHECK(rows >= 0 && K >= 0, GLT_ERR_SHAPE, "shuffle_b: negative shape");
+  if (rows == 0 || K == 0) return GLT_OK;
+  GLT_CHECK(src && dst, GLT_ERR_INVALID_ARG, "shuffle_b: null pointer");
+  const int kblocks = (int)(shuf_k(K) / kShufK);
+  const int64_t blocks = shuf_rows(rows) / kShufRows * kblocks;
+  GLT_CHECK(blocks < (1ll << 31), GLT_ERR_SHAPE, "shuffle_b: %lld blocks", (long long)blocks);
+  const dim3 grid((unsigned)blocks);
+  if (src_dtype == GLT_DTYPE_F32) {
+    const float* s = static_cast<const float*>(src);
+    if (transposed) GLT_LAUNCH("shuffle", (shuffle_kernel<float, true>), grid, dim3(256), 0, st, s, ld, rows, K, kblocks, dst);
+    else GLT_LAUNCH("shuffle", (shuffle_kernel<float, false>), grid, dim3(256), 0, st, s, ld, rows, K, kblocks, dst);
+  } else {
+    const uint16_t* s = static_cast<const uint16_t*>(src);
+    if (transposed) GLT_LAUNCH("shuffle", (shuffle_kernel<uint16_t, true>), grid, dim3(256), 0, st, s, ld, rows, K, kblocks, dst);
+    else GLT_LAUNCH("shuffle", (shuffle_kernel<uint16_t, false>), grid, dim3(256), 0, st, s, ld, rows, K, kblocks, dst);
+  }
+  GLT_LAUNCH_CHECK("shuffle");
+  return GLT_OK;
+}
+
+}  // namespace glt

@@ -5,6 +5,7 @@
 #include <cstdio>
 
 #include "common.hpp"
+#include "layout.hpp"
 
 namespace glt {
 
@@ -142,6 +143,18 @@ glt_status convert_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStr
   return GLT_OK;
 }
 
+glt_status pack_projection(const float* master, int S, int H, int proj, uint16_t* packed, hipStream_t st) {
+  const int64_t sh = (int64_t)S * H;
+  uint16_t* rm = packed + 2 * proj * sh;
+  glt_status s;
+  if ((s = convert_f32_to_bf16(master, rm, sh, st)) != GLT_OK) return s;
+  if ((s = transpose_f32_to_bf16(master, rm + sh, S, H, st)) != GLT_OK) return s;
+  if ((s = shuffle_b(master, GLT_DTYPE_F32, H, false, S, H, packed + packed_shuf_offset(S, H, 2 * proj), st)) !=
+      GLT_OK)
+    return s;
+  return shuffle_b(master, GLT_DTYPE_F32, H, true, H, S, packed + packed_shuf_offset(S, H, 2 * proj + 1), st);
+}
+
 // ------------------------------------------------------ elementwise probes
 // silu(g)*u with the reference's f32 operation order
 // (reference src/kernels_elementwise_impl.inc:395-401): sg = 1/(1+exp(-g)),
@@ -223,18 +236,21 @@ glt_status glt_transpose(const void* src, void* dst, int32_t rows, int32_t cols,
   return transpose_any(src, dst, rows, cols, cols, dtype, as_stream(stream));
 }
 
+size_t glt_graft_packed_size(int32_t S, int32_t H) {
+  if (S <= 0 || H <= 0) return 0;
+  return (size_t)packed_bytes(S, H);
+}
+
 glt_status glt_graft_pack(const glt_graft_slice* sl, uint16_t* packed, void* stream) {
   GLT_CHECK(sl && packed, GLT_ERR_INVALID_ARG, "glt_graft_pack: null pointer");
   GLT_CHECK(sl->s > 0 && sl->h > 0, GLT_ERR_SHAPE, "glt_graft_pack: empty slice");
-  const int64_t sh = (int64_t)sl->s * sl->h;
+  GLT_CHECK((reinterpret_cast<uintptr_t>(packed) & 255) == 0, GLT_ERR_ALIGNMENT,
+            "glt_graft_pack: packed buffer must be 256-byte aligned");
   const float* masters[3] = {sl->master_gate, sl->master_up, sl->master_down};
   hipStream_t st = as_stream(stream);
   for (int p = 0; p < 3; ++p) {
     if (!masters[p]) continue;
-    uint16_t* base = packed + 2 * p * sh;
-    glt_status s = convert_f32_to_bf16(masters[p], base, sh, st);
-    if (s != GLT_OK) return s;
-    s = transpose_f32_to_bf16(masters[p], base + sh, sl->s, sl->h, st);
+    glt_status s = pack_projection(masters[p], sl->s, sl->h, p, packed, st);
     if (s != GLT_OK) return s;
   }
   return GLT_OK;

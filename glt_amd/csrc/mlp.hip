@@ -4,6 +4,7 @@
 #include <algorithm>
 
 #include "gemm.hpp"
+#include "layout.hpp"
 
 namespace glt {
 
@@ -13,11 +14,32 @@ glt_status transpose_any(const void* src, void* dst, int rows, int cols, int64_t
 static size_t esize(int dtype) { return dtype == GLT_DTYPE_F32 ? 4 : 2; }
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Packed bf16 mirror sub-blocks (glt_graft_slice.packed):
-// gate[S,H], gate^T[H,S], up[S,H], up^T[H,S], down[S,H], down^T[H,S].
+// Row-major packed-mirror orientation q = 2*proj + transposed (layout.hpp).
 static const uint16_t* packed_block(const glt_graft_slice& s, int proj, bool transposed) {
   const int64_t sh = (int64_t)s.s * s.h;
   return s.packed + (2 * proj + (transposed ? 1 : 0)) * sh;
+}
+// Shuffled packed-mirror orientation.
+static const uint16_t* packed_shuf(const glt_graft_slice& s, int proj, bool transposed) {
+  return s.packed + packed_shuf_offset(s.s, s.h, 2 * proj + (transposed ? 1 : 0));
+}
+static const uint16_t* prep(const glt_mlp_desc* d, const glt_base_weights* w, int slot) {
+  return static_cast<const uint16_t*>(w->prepared) + prep_offset(d->I, d->D, slot);
+}
+
+// The bf16 MLP runs on the MFMA kernel when every K is a multiple of 64,
+// every output column range and every operand row offset is 32-aligned
+// (whole shuffled B blocks) and the activation rows are 16-byte aligned;
+// other shapes (and the f32 path) take the strided generic kernel.
+static bool mlp_uses_mfma(const glt_mlp_desc* d) {
+  if (d->dtype != GLT_DTYPE_BF16) return false;
+  if (d->D % 64 || d->I % 64 || d->N % 8) return false;
+  if (d->flags & GLT_MLP_EXPLICIT)
+    for (int j = 0; j < d->n_slices; ++j) {
+      const glt_graft_slice& s = d->slices[j];
+      if (s.s % 64 || s.h % 64 || s.i_start % 32 || s.h_start % 32) return false;
+    }
+  return true;
 }
 
 static glt_status check_desc(const glt_mlp_desc* d, const glt_base_weights* w, const char* who) {
@@ -28,6 +50,8 @@ static glt_status check_desc(const glt_mlp_desc* d, const glt_base_weights* w, c
   GLT_CHECK(d->n_slices >= 0 && d->n_slices <= 7, GLT_ERR_UNSUPPORTED, "%s: %d slices (max 7)", who, d->n_slices);
   GLT_CHECK(d->n_slices == 0 || d->slices, GLT_ERR_INVALID_ARG, "%s: null slices", who);
   GLT_CHECK(d->I == 0 || (w->gate && w->up && w->down), GLT_ERR_INVALID_ARG, "%s: null base weight", who);
+  GLT_CHECK(d->I == 0 || !mlp_uses_mfma(d) || w->prepared, GLT_ERR_INVALID_ARG,
+            "%s: the bf16 path needs the prepared base (glt_base_prepare)", who);
   const bool explicit_graft = d->flags & GLT_MLP_EXPLICIT;
   for (int j = 0; explicit_graft && j < d->n_slices; ++j) {
     const glt_graft_slice& s = d->slices[j];
@@ -58,22 +82,41 @@ static GProb prob(int M, int N, int mode, bool f32, void* o0, void* o1, void* o2
   return p;
 }
 
+// Operand kinds of a plan: MFMA path = bf16 A, shuffled B; otherwise the
+// path dtype, strided.
+static void set_kinds(GemmPlan& plan, const glt_mlp_desc* d, bool mfma) {
+  plan.a_kind = d->dtype == GLT_DTYPE_F32 ? LD_F32 : LD_BF16;
+  plan.b_kind = mfma ? LD_SHUF : plan.a_kind;
+}
+
 // gate/up concat-N GEMM with the SiLU*up epilogue.
 static glt_status gate_up_forward(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, void* g_out,
                                   void* u_out, void* inter, hipStream_t st) {
   const bool f32 = d->dtype == GLT_DTYPE_F32;
+  const bool mfma = mlp_uses_mfma(d);
   GemmPlan plan;
   plan.dual = true;
   plan.label = "gate_up";
-  plan.a_kind = plan.b_kind = f32 ? LD_F32 : LD_BF16;
+  set_kinds(plan, d, mfma);
   plan.add_problem(prob(d->M, d->N, EPI_SILU, f32, inter, g_out, u_out, d->N));
-  if (d->I > 0) plan.add_seg(nt_seg(x, d->D, 0, d->D, 0, d->I, w->gate, d->D, 0, w->up, d->D, 0));
+  if (d->I > 0) {
+    if (mfma)
+      plan.add_seg(nt_seg(x, d->D, 0, d->D, 0, d->I, prep(d, w, PREP_GATE), d->D, 0, prep(d, w, PREP_UP), d->D, 0));
+    else
+      plan.add_seg(nt_seg(x, d->D, 0, d->D, 0, d->I, w->gate, d->D, 0, w->up, d->D, 0));
+  }
   if (d->flags & GLT_MLP_EXPLICIT) {
     for (int j = 0; j < d->n_slices; ++j) {
       const glt_graft_slice& s = d->slices[j];
       if (!s.master_gate && !s.master_up) continue;
-      const void* bg = f32 ? (const void*)s.master_gate : (s.master_gate ? packed_block(s, 0, false) : nullptr);
-      const void* bu = f32 ? (const void*)s.master_up : (s.master_up ? packed_block(s, 1, false) : nullptr);
+      const void *bg, *bu;
+      if (mfma) {
+        bg = s.master_gate ? packed_shuf(s, 0, false) : nullptr;
+        bu = s.master_up ? packed_shuf(s, 1, false) : nullptr;
+      } else {
+        bg = f32 ? (const void*)s.master_gate : (s.master_gate ? packed_block(s, 0, false) : nullptr);
+        bu = f32 ? (const void*)s.master_up : (s.master_up ? packed_block(s, 1, false) : nullptr);
+      }
       plan.add_seg(nt_seg(x, d->D, s.h_start, s.h, s.i_start, s.i_start + s.s, bg, s.h, s.i_start, bu, s.h,
                           s.i_start));
     }
@@ -85,11 +128,12 @@ static glt_status gate_up_forward(const glt_mlp_desc* d, const glt_base_weights*
 static glt_status down_forward(const glt_mlp_desc* d, const glt_base_weights* w, const void* inter, void* y,
                                hipStream_t st) {
   const bool f32 = d->dtype == GLT_DTYPE_F32;
+  const bool mfma = mlp_uses_mfma(d);
   GemmPlan plan;
   plan.label = "down";
-  plan.a_kind = plan.b_kind = f32 ? LD_F32 : LD_BF16;
+  set_kinds(plan, d, mfma);
   plan.add_problem(prob(d->M, d->D, EPI_STORE, f32, y, nullptr, nullptr, d->D));
-  if (d->I > 0) plan.add_seg(nt_seg(inter, d->N, 0, d->I, 0, d->D, w->down, d->I, 0));
+  if (d->I > 0) plan.add_seg(nt_seg(inter, d->N, 0, d->I, 0, d->D, mfma ? prep(d, w, PREP_DOWN) : w->down, d->I, 0));
   if (d->flags & GLT_MLP_EXPLICIT) {
     for (int j = 0; j < d->n_slices; ++j) {
       const glt_graft_slice& s = d->slices[j];
@@ -100,8 +144,8 @@ static glt_status down_forward(const glt_mlp_desc* d, const glt_base_weights* w,
         g.b_ks = s.h;
         plan.add_seg(g);
       } else {
-        plan.add_seg(nt_seg(inter, d->N, s.i_start, s.s, s.h_start, s.h_start + s.h, packed_block(s, 2, true), s.s,
-                            s.h_start));
+        plan.add_seg(nt_seg(inter, d->N, s.i_start, s.s, s.h_start, s.h_start + s.h,
+                            mfma ? packed_shuf(s, 2, true) : packed_block(s, 2, true), s.s, s.h_start));
       }
     }
   }
@@ -110,27 +154,18 @@ static glt_status down_forward(const glt_mlp_desc* d, const glt_base_weights* w,
 
 struct BwdLayout {
   size_t dg, du, xt, dyt, g, u, inter, slice0, slice_stride, total;
-  bool mfma;
+  bool wgrad_mfma;
 };
 
-// MFMA eligibility of the backward's NT GEMMs depends only on alignment,
-// which the workspace layout and these checks settle up front.
-static bool bwd_uses_mfma(const glt_mlp_desc* d) {
-  if (d->dtype != GLT_DTYPE_BF16) return false;
-  if (d->D % 64 || d->I % 64 || d->N % 8 || d->M % 64) return false;
-  if (d->flags & GLT_MLP_EXPLICIT)
-    for (int j = 0; j < d->n_slices; ++j) {
-      const glt_graft_slice& s = d->slices[j];
-      if (s.s % 64 || s.h % 64 || s.i_start % 8 || s.h_start % 8) return false;
-    }
-  return true;
-}
+// The weight gradients reduce over the M tokens; on the MFMA kernel that K
+// must be a multiple of 64 as well.
+static bool wgrad_uses_mfma(const glt_mlp_desc* d) { return mlp_uses_mfma(d) && d->M % 64 == 0; }
 
 static BwdLayout bwd_layout(const glt_mlp_desc* d) {
   BwdLayout L{};
   const size_t es = esize(d->dtype);
-  const size_t MN = (size_t)d->M * d->N * es, MD = (size_t)d->M * d->D * es;
-  L.mfma = bwd_uses_mfma(d);
+  const size_t MN = (size_t)d->M * d->N * es;
+  L.wgrad_mfma = wgrad_uses_mfma(d);
   size_t off = 0;
   L.dg = off; off += align256(MN);
   L.du = off; off += align256(MN);
@@ -139,15 +174,16 @@ static BwdLayout bwd_layout(const glt_mlp_desc* d) {
     L.u = off; off += align256(MN);
     L.inter = off; off += align256(MN);
   }
-  if (L.mfma) {
-    L.xt = off; off += align256(MD);
-    L.dyt = off; off += align256(MD);
+  const bool grads = (d->flags & GLT_MLP_EXPLICIT) && d->n_slices > 0;
+  if (L.wgrad_mfma && grads) {
+    // x and dy as shuffled B operands [D rows, K = M]
+    L.xt = off; off += align256((size_t)shuf_elems(d->D, d->M) * 2);
+    L.dyt = off; off += align256((size_t)shuf_elems(d->D, d->M) * 2);
     L.slice0 = off;
     size_t per = 0;
-    for (int j = 0; (d->flags & GLT_MLP_EXPLICIT) && j < d->n_slices; ++j)
-      per = std::max(per, 3 * align256((size_t)d->slices[j].s * d->M * es));
+    for (int j = 0; j < d->n_slices; ++j) per = std::max(per, 3 * align256((size_t)d->slices[j].s * d->M * es));
     L.slice_stride = per;
-    off += per * (size_t)((d->flags & GLT_MLP_EXPLICIT) ? d->n_slices : 0);
+    off += per * (size_t)d->n_slices;
   }
   L.total = off;
   return L;
@@ -159,17 +195,34 @@ using namespace glt;
 
 extern "C" {
 
+size_t glt_base_prepared_size(const glt_mlp_desc* d) {
+  if (!d || d->dtype != GLT_DTYPE_BF16 || d->I <= 0 || d->D <= 0) return 0;
+  return (size_t)prep_bytes(d->I, d->D);
+}
+
 glt_status glt_base_prepare(const glt_mlp_desc* d, const void* gate, const void* up, const void* down,
-                            void* gate_t, void* up_t, void* down_t, void* stream) {
-  GLT_CHECK(d && gate && up && down && gate_t && up_t && down_t, GLT_ERR_INVALID_ARG,
-            "glt_base_prepare: null pointer");
+                            void* prepared, void* stream) {
+  GLT_CHECK(d, GLT_ERR_INVALID_ARG, "glt_base_prepare: null descriptor");
   GLT_CHECK(d->dtype == GLT_DTYPE_BF16 || d->dtype == GLT_DTYPE_F32, GLT_ERR_DTYPE, "glt_base_prepare: dtype");
   GLT_CHECK(d->D > 0 && d->I >= 0, GLT_ERR_SHAPE, "glt_base_prepare: dims");
+  if (d->dtype == GLT_DTYPE_F32 || d->I == 0) return GLT_OK;  // the f32 path reads the base as is
+  GLT_CHECK(gate && up && down && prepared, GLT_ERR_INVALID_ARG, "glt_base_prepare: null pointer");
+  GLT_CHECK((reinterpret_cast<uintptr_t>(prepared) & 255) == 0, GLT_ERR_ALIGNMENT,
+            "glt_base_prepare: prepared buffer must be 256-byte aligned");
   hipStream_t st = as_stream(stream);
-  glt_status s;
-  if ((s = transpose_any(gate, gate_t, d->I, d->D, d->D, d->dtype, st)) != GLT_OK) return s;
-  if ((s = transpose_any(up, up_t, d->I, d->D, d->D, d->dtype, st)) != GLT_OK) return s;
-  return transpose_any(down, down_t, d->D, d->I, d->I, d->dtype, st);
+  uint16_t* out = static_cast<uint16_t*>(prepared);
+  const int I = d->I, D = d->D;
+  struct Job { const void* src; int64_t ld; bool tr; int rows, K; };
+  const Job jobs[6] = {
+      {gate, D, false, I, D}, {up, D, false, I, D}, {down, I, false, D, I},
+      {down, I, true, I, D},  {gate, D, true, D, I}, {up, D, true, D, I},
+  };
+  for (int q = 0; q < 6; ++q) {
+    glt_status s = shuffle_b(jobs[q].src, GLT_DTYPE_BF16, jobs[q].ld, jobs[q].tr, jobs[q].rows, jobs[q].K,
+                             out + prep_offset(I, D, q), st);
+    if (s != GLT_OK) return s;
+  }
+  return GLT_OK;
 }
 
 glt_status glt_mlp_fwd(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, void* y, void* gate_pre,
@@ -204,13 +257,10 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
   GLT_CHECK(ws_bytes >= L.total && (L.total == 0 || ws), GLT_ERR_WORKSPACE,
             "glt_mlp_bwd: workspace %zu bytes < required %zu", ws_bytes, L.total);
   if (d->M == 0) return GLT_OK;
-  GLT_CHECK(d->I == 0 || w->down_t || !L.mfma, GLT_ERR_INVALID_ARG,
-            "glt_mlp_bwd: bf16 path needs the transposed base (glt_base_prepare)");
-  GLT_CHECK(d->I == 0 || !L.mfma || (w->gate_t && w->up_t), GLT_ERR_INVALID_ARG,
-            "glt_mlp_bwd: bf16 path needs the transposed base (glt_base_prepare)");
   hipStream_t st = as_stream(stream);
   char* W = static_cast<char*>(ws);
   const bool f32 = d->dtype == GLT_DTYPE_F32;
+  const bool mfma = mlp_uses_mfma(d);
   const int kind = f32 ? LD_F32 : LD_BF16;
   const int dt = d->dtype;
   const int M = d->M, D = d->D, I = d->I, N = d->N;
@@ -229,11 +279,11 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
   {
     GemmPlan plan;
     plan.label = "dinter";
-    plan.a_kind = plan.b_kind = kind;
+    set_kinds(plan, d, mfma);
     plan.add_problem(prob(M, N, EPI_DGDU, f32, dg, du, nullptr, N, gate_pre, up_pre, N));
     if (I > 0) {
-      if (w->down_t) {
-        plan.add_seg(nt_seg(dy, D, 0, D, 0, I, w->down_t, D, 0));
+      if (mfma) {
+        plan.add_seg(nt_seg(dy, D, 0, D, 0, I, prep(d, w, PREP_DOWN_T), D, 0));
       } else {
         GSeg g = nt_seg(dy, D, 0, D, 0, I, w->down, 1, 0);  // B(n, k) = W_down[k, n]
         g.b_ks = I;
@@ -244,7 +294,7 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
       const glt_graft_slice& sl = d->slices[j];
       if (!sl.master_down) continue;
       // B(n = i0+s, k = h) = delta_down[s, h]: the [S,H] storage is NT as is
-      const void* B = f32 ? (const void*)sl.master_down : packed_block(sl, 2, false);
+      const void* B = f32 ? (const void*)sl.master_down : mfma ? packed_shuf(sl, 2, false) : packed_block(sl, 2, false);
       plan.add_seg(nt_seg(dy, D, sl.h_start, sl.h, sl.i_start, sl.i_start + sl.s, B, sl.h, sl.i_start));
     }
     if ((s = run_gemm(plan, st)) != GLT_OK) return s;
@@ -255,15 +305,15 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
   if (dx) {
     GemmPlan plan;
     plan.label = "dx";
-    plan.a_kind = plan.b_kind = kind;
+    set_kinds(plan, d, mfma);
     plan.add_problem(prob(M, D, EPI_STORE, true, dx, nullptr, nullptr, D));
     if (I > 0) {
-      const void* wt[2] = {w->gate_t, w->up_t};
+      const int slots[2] = {PREP_GATE_T, PREP_UP_T};
       const void* wo[2] = {w->gate, w->up};
       const void* a[2] = {dg, du};
       for (int p = 0; p < 2; ++p) {
-        if (wt[p]) {
-          plan.add_seg(nt_seg(a[p], N, 0, I, 0, D, wt[p], I, 0));
+        if (mfma) {
+          plan.add_seg(nt_seg(a[p], N, 0, I, 0, D, prep(d, w, slots[p]), I, 0));
         } else {
           GSeg g = nt_seg(a[p], N, 0, I, 0, D, wo[p], 1, 0);  // B(n, k) = W[k, n]
           g.b_ks = D;
@@ -282,8 +332,8 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
           g.b_ks = sl.h;  // B(n = h0+h, k = s) = delta[s, h]
           plan.add_seg(g);
         } else {
-          plan.add_seg(nt_seg(a[p], N, sl.i_start, sl.s, sl.h_start, sl.h_start + sl.h, packed_block(sl, p, true),
-                              sl.s, sl.h_start));
+          plan.add_seg(nt_seg(a[p], N, sl.i_start, sl.s, sl.h_start, sl.h_start + sl.h,
+                              mfma ? packed_shuf(sl, p, true) : packed_block(sl, p, true), sl.s, sl.h_start));
         }
       }
     }
@@ -294,16 +344,18 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
   //    (reference src/graft_ops_impl.inc:120-141, :214-228):
   //      dGate = dgate_i^T . x_h, dUp = dup_i^T . x_h, dDown = inter_i^T . dy_h
   if (!explicit_graft || d->n_slices == 0) return GLT_OK;
-  if (L.mfma) {
-    // K (= tokens) must be the contiguous axis of both operands for the MFMA
-    // kernel: transpose x, dy and each slice's column blocks once.
-    char* XT = W + L.xt;
-    char* DYT = W + L.dyt;
-    if ((s = transpose_any(x, XT, M, D, D, dt, st)) != GLT_OK) return s;
-    if ((s = transpose_any(dy, DYT, M, D, D, dt, st)) != GLT_OK) return s;
+  if (L.wgrad_mfma) {
+    // K (= tokens) must be the contiguous axis of A: each slice's column
+    // block of dgate/dup/inter is transposed once; x and dy become shuffled
+    // B operands [D rows, K = M] once for all slices.
+    uint16_t* XS = reinterpret_cast<uint16_t*>(W + L.xt);
+    uint16_t* DYS = reinterpret_cast<uint16_t*>(W + L.dyt);
+    if ((s = shuffle_b(x, dt, D, true, D, M, XS, st)) != GLT_OK) return s;
+    if ((s = shuffle_b(dy, dt, D, true, D, M, DYS, st)) != GLT_OK) return s;
     GemmPlan plan;
     plan.label = "wgrad";
-    plan.a_kind = plan.b_kind = LD_BF16;
+    plan.a_kind = LD_BF16;
+    plan.b_kind = LD_SHUF;
     const size_t es = esize(dt);
     for (int j = 0; j < d->n_slices; ++j) {
       const glt_graft_slice& sl = d->slices[j];
@@ -317,15 +369,16 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
         if (!outs[p] || !mast[p]) continue;
         char* AT = base + p * blk;
         if ((s = transpose_any(srcs[p] + (size_t)sl.i_start * es, AT, M, sl.s, N, dt, st)) != GLT_OK) return s;
-        const char* BT = (p < 2 ? XT : DYT) + (size_t)sl.h_start * M * es;
         if (plan.args.nprob == kMaxProb) {
           if ((s = run_gemm(plan, st)) != GLT_OK) return s;
           plan = GemmPlan();
           plan.label = "wgrad";
-          plan.a_kind = plan.b_kind = LD_BF16;
+          plan.a_kind = LD_BF16;
+          plan.b_kind = LD_SHUF;
         }
+        // B row of output column h is row h0 + h of the shuffled x / dy
         plan.add_problem(prob(sl.s, sl.h, EPI_STORE, true, outs[p], nullptr, nullptr, sl.h));
-        plan.add_seg(nt_seg(AT, M, 0, M, 0, sl.h, BT, M, 0));
+        plan.add_seg(nt_seg(AT, M, 0, M, 0, sl.h, p < 2 ? XS : DYS, M, -sl.h_start));
       }
     }
     return run_gemm(plan, st);

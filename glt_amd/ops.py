@@ -40,8 +40,8 @@ def delta_offset(layer_idx, proj_idx, slice_dim, h_slice_dim):
 
 class GraftSlice:
     """One graft slice of one layer: placement + f32 masters [S,H] + the
-    packed bf16 mirror both orientations (reference GraftWeights,
-    src/types.hpp:190-201)."""
+    packed bf16 mirror (every orientation the GEMMs read; reference
+    GraftWeights, src/types.hpp:190-201)."""
 
     def __init__(self, i_start, s, h_start, h, gate=None, up=None, down=None):
         self.i_start, self.s, self.h_start, self.h = int(i_start), int(s), int(h_start), int(h)
@@ -51,7 +51,8 @@ class GraftSlice:
                 assert t.dtype == torch.float32 and tuple(t.shape) == (self.s, self.h) and t.is_contiguous()
         dev = next(t.device for t in (gate, up, down) if t is not None) if any(
             t is not None for t in (gate, up, down)) else torch.device("cuda")
-        self.packed = torch.zeros(6 * self.s * self.h, dtype=torch.bfloat16, device=dev)
+        nbytes = F.load().glt_graft_packed_size(self.s, self.h)
+        self.packed = torch.zeros(nbytes // 2, dtype=torch.bfloat16, device=dev)
 
     def c_struct(self):
         return F.GraftSlice(self.i_start, self.s, self.h_start, self.h, _p(self.gate), _p(self.up), _p(self.down),
@@ -74,28 +75,28 @@ def _slices_array(slices):
 
 class BaseMLP:
     """Frozen base weights of one MLP layer: gate/up [I,D], down [D,I], plus
-    the transposed copies the backward GEMMs read (made once)."""
+    (bf16) the prepared copy the GEMMs read, made once."""
 
     def __init__(self, gate, up, down, prepare=True):
         self.gate, self.up, self.down = gate, up, down
         self.I, self.D = gate.shape
         self.dtype = gate.dtype
-        self.gate_t = self.up_t = self.down_t = None
+        self.prepared = None
         if prepare and self.I > 0:
             self.prepare()
 
     def prepare(self):
-        self.gate_t = torch.empty((self.D, self.I), dtype=self.dtype, device=self.gate.device)
-        self.up_t = torch.empty_like(self.gate_t)
-        self.down_t = torch.empty((self.I, self.D), dtype=self.dtype, device=self.gate.device)
         d = F.MlpDesc(0, self.D, self.I, self.I, _dtype_code(self.dtype), 0, 0, None, None)
-        F.call("glt_base_prepare", ctypes.byref(d), _p(self.gate), _p(self.up), _p(self.down), _p(self.gate_t),
-               _p(self.up_t), _p(self.down_t), _stream())
+        nbytes = F.load().glt_base_prepared_size(ctypes.byref(d))
+        if nbytes == 0:
+            return self
+        self.prepared = torch.empty(nbytes, dtype=torch.uint8, device=self.gate.device)
+        F.call("glt_base_prepare", ctypes.byref(d), _p(self.gate), _p(self.up), _p(self.down), _p(self.prepared),
+               _stream())
         return self
 
     def c_struct(self):
-        return F.BaseWeights(_p(self.gate), _p(self.up), _p(self.down), _p(self.gate_t), _p(self.up_t),
-                             _p(self.down_t))
+        return F.BaseWeights(_p(self.gate), _p(self.up), _p(self.down), _p(self.prepared))
 
 
 def _desc(base, slices, M, N, explicit, recompute=False, state=None):

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GLT_ABI_VERSION 1
+#define GLT_ABI_VERSION 2
 
 /* ------------------------------------------------------------------ status */
 typedef int32_t glt_status;
@@ -70,9 +70,11 @@ typedef struct {
  *
  * master_*: f32 [S,H] master deltas (reference GraftWeights.d_weight,
  *           src/types.hpp:190-201). NULL = projection not grafted.
- * packed:   bf16 mirror written by glt_graft_pack / glt_adamw_step, 6*S*H
- *           elements: gate[S,H], gate^T[H,S], up[S,H], up^T[H,S],
- *           down[S,H], down^T[H,S]. Read by the bf16 path; unused by f32.  */
+ * packed:   bf16 mirror written by glt_graft_pack / glt_adamw_graft_step,
+ *           glt_graft_packed_size(S, H) bytes, 256-byte aligned: the six
+ *           orientations gate[S,H], gate^T[H,S], up[S,H], up^T[H,S],
+ *           down[S,H], down^T[H,S] row-major, then the same six in the
+ *           MFMA fragment layout. Read by the bf16 path; unused by f32.  */
 typedef struct {
   int32_t i_start, s, h_start, h;
   const float* master_gate;
@@ -90,17 +92,18 @@ typedef struct {
   float* down;
 } glt_graft_grads;
 
-/* Frozen base weights of one MLP layer (torch Linear [out,in] layout).
- * gate/up [I,D], down [D,I]. The *_t copies are the transposes used by the
- * backward GEMMs (gate_t/up_t [D,I], down_t [I,D]); glt_base_prepare makes
- * them once per frozen base. dtype = the path dtype. */
+/* Frozen base weights of one MLP layer (torch Linear [out,in] layout),
+ * gate/up [I,D], down [D,I], in the path dtype. prepared: the bf16 path's
+ * copy of all six orientations the GEMMs multiply by (gate, up, down,
+ * down^T, gate^T, up^T) in the MFMA fragment layout, made once per frozen
+ * base by glt_base_prepare (glt_base_prepared_size bytes); NULL on the f32
+ * path. It replaces the reference's cached f32 base copies
+ * (src/model_io_impl.inc:174-177). */
 typedef struct {
   const void* gate;
   const void* up;
   const void* down;
-  const void* gate_t;
-  const void* up_t;
-  const void* down_t;
+  const void* prepared;
 } glt_base_weights;
 
 /* Shape of one grafted SwiGLU MLP call.
@@ -155,17 +158,22 @@ glt_status glt_fill_normal(void* out, int32_t dtype, int64_t n, uint64_t seed,
                            void* stream);
 
 /* --------------------------------------------------------------- graft ops */
-/* Build the bf16 mirror of one slice (both orientations) from its f32 masters.
+/* Bytes of the packed bf16 mirror of an S x H slice (glt_graft_slice.packed). */
+size_t glt_graft_packed_size(int32_t S, int32_t H);
+/* Build the packed bf16 mirror of one slice from its f32 masters.
  * Replaces refresh_graft_weight_bf16 / convert_f32_to_bf16 of the reference
  * (src/gemm_impl.inc:85-95), which it ran before every graft GEMM call. */
 glt_status glt_graft_pack(const glt_graft_slice* slice, uint16_t* packed, void* stream);
 
-/* Transposed copies of a frozen base (dst[c,r] = src[r,c]), rows x cols. */
+/* Transposed copy (dst[c,r] = src[r,c]), rows x cols. */
 glt_status glt_transpose(const void* src, void* dst, int32_t rows, int32_t cols,
                          int32_t dtype, void* stream);
+/* Bytes of glt_base_weights.prepared for d (0 on the f32 path). */
+size_t glt_base_prepared_size(const glt_mlp_desc* d);
+/* Writes the prepared copy of a frozen bf16 base (256-byte aligned buffer);
+ * a no-op on the f32 path. */
 glt_status glt_base_prepare(const glt_mlp_desc* d, const void* gate, const void* up,
-                            const void* down, void* gate_t, void* up_t, void* down_t,
-                            void* stream);
+                            const void* down, void* prepared, void* stream);
 
 /* The six graft GEMM kinds of the reference (src/config.hpp:31-38,
  * graft_gemm_fwd / grad_gemm / grad_gemm_storage_canonical
@@ -270,8 +278,8 @@ glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* bf16
                           size_t ws_bytes, void* stream);
 
 /* AdamW over a whole graft set with the packed-mirror refresh fused in:
- * updates each slice's masters (treated as writable) and rewrites its
- * packed bf16 mirror in both orientations. grads/m/v are per-slice [3,S,H]
+ * updates each slice's masters (treated as writable) and rewrites the
+ * updated projections' part of its packed bf16 mirror. grads/m/v are per-slice [3,S,H]
  * f32 buffers laid out gate,up,down. proj_mask as in the reference
  * (skipped projections are untouched, src/kernels_optimizer_impl.inc:20-25). */
 glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,

@@ -66,3 +66,32 @@ def make_layer(D, I, N, slices_pl, bf16=True, base_seed=0, graft_std=0.02):
             sd[name] = synth.normal((s, h), k + 1, 1 + p, 0, graft_std)  # f32 masters
         slices.append(sd)
     return wg, wu, wd, slices
+
+
+def shuffle_b(b):
+    """The MFMA fragment layout of a B operand [rows, K] (the kernels' own
+    weight format, written by glt_base_prepare / glt_graft_pack): 32 x 64
+    blocks, row-block major; inside a block [substep 4][lane 64][8], lane l
+    of substep s holding row l%32, K = 16*s + 8*(l//32) + e. Zero padded."""
+    b = np.asarray(b, np.float32)
+    rows, k = b.shape
+    rp, kp = -(-rows // 32) * 32, -(-k // 64) * 64
+    pad = np.zeros((rp, kp), np.float32)
+    pad[:rows, :k] = b
+    blk = pad.reshape(rp // 32, 32, kp // 64, 4, 2, 8)  # rb, r, kb, s, half, e
+    return blk.transpose(0, 2, 3, 4, 1, 5).reshape(-1)
+
+
+def packed_views(packed_f32, s, h):
+    """Splits a packed graft mirror (as f32 values) into its six row-major
+    orientations and six shuffled ones (gate, gate^T, up, up^T, down, down^T)."""
+    sh = s * h
+    rowmajor = [packed_f32[q * sh:(q + 1) * sh].reshape((h, s) if q & 1 else (s, h)) for q in range(6)]
+    off = -(-6 * sh // 128) * 128
+    shuf = []
+    for q in range(6):
+        r, k = (h, s) if q & 1 else (s, h)
+        n = (-(-r // 32) * 32) * (-(-k // 64) * 64)
+        shuf.append(packed_f32[off:off + n])
+        off += n
+    return rowmajor, shuf

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from glt_amd import _ffi
     lib = _ffi.load()
-    assert lib.glt_version() == 1
+    assert lib.glt_version() == 2
     assert isinstance(lib.glt_last_error_string(), bytes)
 
 
@@ -41,7 +41,7 @@ def test_host_validation_errors_without_gpu():
     lib = F.load()
     st = F.ModelState(1)
     d = F.MlpDesc(16, 64, 64, 64, F.DTYPE_BF16, F.MLP_EXPLICIT, 0, None, ctypes.pointer(st))
-    w = F.BaseWeights(1, 1, 1, 1, 1, 1)
+    w = F.BaseWeights(1, 1, 1, 1)
     rc = lib.glt_mlp_bwd(ctypes.byref(d), ctypes.byref(w), 1, 1, 1, 1, 1, None, None, None, 0, None)
     assert rc == 7  # GLT_ERR_BAKED_NO_BACKWARD (reference src/layer_backward_impl.inc:11-13)
     bd = F.BakeDesc(0, 1, 0, 0, 7, 64, 64, 64, F.DTYPE_F32, 0, None, None)

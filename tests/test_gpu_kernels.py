@@ -3,7 +3,8 @@ elementwise probes, conversions) and the graft-GEMM kinds."""
 import numpy as np
 import pytest
 
-from helpers import assert_bf16_budget, assert_f32_close, draw, rel_l2, to_dev, to_np
+from helpers import (assert_bf16_budget, assert_f32_close, draw, packed_views, rel_l2, shuffle_b, to_dev,
+                     to_np)
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -232,13 +233,38 @@ def test_adamw_graft_step_refreshes_packed_mirror(dev):
     ops.adamw_graft_step([sl], [grads], [m], [v], 0, 1e-4)
     torch.cuda.synchronize()
     gn = to_np(grads).reshape(3, S, H)
-    pk = O.bf16_bits_to_f32(_bits(sl.packed)).reshape(6, -1)
+    rowmajor, shuf = packed_views(O.bf16_bits_to_f32(_bits(sl.packed)), S, H)
     for p in range(3):
         rw, _, _ = O.adamw(w0[p], gn[p], np.zeros((S, H), np.float32), np.zeros((S, H), np.float32), 0, 1e-4,
                            0.9, 0.999, 1e-8, 0.01)
         assert_f32_close(to_np(ms[p]), rw, tol=1e-6)
-        np.testing.assert_array_equal(pk[2 * p].reshape(S, H), O.bf16_round(to_np(ms[p])))
-        np.testing.assert_array_equal(pk[2 * p + 1].reshape(H, S), O.bf16_round(to_np(ms[p])).T)
+        wb = O.bf16_round(to_np(ms[p]))
+        np.testing.assert_array_equal(rowmajor[2 * p], wb)
+        np.testing.assert_array_equal(rowmajor[2 * p + 1], wb.T)
+        np.testing.assert_array_equal(shuf[2 * p], shuffle_b(wb))
+        np.testing.assert_array_equal(shuf[2 * p + 1], shuffle_b(wb.T))
+
+
+def test_base_prepare_layout(dev):
+    """The prepared base holds gate, up, down, down^T, gate^T, up^T in the
+    fragment layout, bit for bit (ragged sizes pad with zeros)."""
+    import ctypes
+    import torch
+    from glt_amd import _ffi as F
+    from glt_amd import ops
+    I, D = 96, 80
+    wg = draw((I, D), 0, 1, 0, 0.02)
+    wu = draw((I, D), 0, 2, 0, 0.02)
+    wd = draw((D, I), 0, 3, 0, 0.02)
+    base = ops.BaseMLP(*(to_dev(a, torch.bfloat16) for a in (wg, wu, wd)))
+    torch.cuda.synchronize()
+    got = O.bf16_bits_to_f32(_bits(base.prepared.view(torch.bfloat16)))
+    off = 0
+    for ref in (wg, wu, wd, wd.T, wg.T, wu.T):
+        exp = shuffle_b(ref)
+        np.testing.assert_array_equal(got[off:off + exp.size], exp)
+        off += exp.size
+    assert off * 2 == base.prepared.numel()
 
 
 # -------------------------------------------------------------- elementwise

@@ -48,6 +48,29 @@ def test_mfma_appended_bf16(dev, M, D, I, S):
         assert_bf16_budget(r["grads"][0][p], r["rgrads"][0][p], q=4, what=f"dW_{name}")
 
 
+def test_mfma_many_tiles_per_workgroup(dev):
+    """More tiles than CUs (576 gate/up, 288 dInter tiles) with a ragged last
+    M-tile: the persistent kernel carries its load stream across tiles."""
+    M, D, I, S = 2112, 512, 7936, 256
+    N = I + S
+    r = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=True)
+    for k, q in (("g", 2), ("u", 2), ("inter", 3), ("y", 4), ("dx", 4)):
+        assert_bf16_budget(*r[k], q=q, what=k)
+    for p, name in enumerate(("gate", "up", "down")):
+        assert_bf16_budget(r["grads"][0][p], r["rgrads"][0][p], q=4, what=f"dW_{name}")
+
+
+def test_mfma_many_tiles_explicit_off(dev):
+    """Graft columns without a segment (explicit off) are zero-K tiles
+    interleaved with full ones in each workgroup's tile sequence."""
+    M, D, I, S = 1024, 256, 7936, 2048
+    N = I + S
+    r = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=True, explicit=False)
+    for k, q in (("g", 2), ("u", 2), ("inter", 3), ("y", 4), ("dx", 4)):
+        assert_bf16_budget(*r[k], q=q, what=k)
+    assert np.all(r["inter"][0][:, I:] == 0)
+
+
 def test_mfma_inplace_and_stacked_bf16(dev):
     """In-place slices (domain-sliced, the reference's CLI form) plus an
     appended slice, all on the MFMA path (64-aligned)."""
