@@ -8,6 +8,25 @@
 namespace glt {
 
 // ---------------------------------------------------------------- epilogue
+// GEMM outputs are rounded with the gfx950 conversion instruction: round to
+// nearest even, the same result as the reference's bias-and-shift rounding
+// (src/kernels_elementwise_impl.inc:570-580) for every finite value. (The
+// bit-exact conversion entry points keep the reference's integer form,
+// which also fixes what NaN payloads become.)
+__device__ __forceinline__ uint16_t bf16_hw(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+__device__ __forceinline__ uint32_t pack2_hw(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// sigmoid 1/(1+exp(-g)) from the hardware exp2 and reciprocal (each within
+// about 1 ulp in f32) instead of the correctly rounded library sequences,
+// which cost some 30 instructions per element in the epilogues; the values
+// are rounded to the path dtype right after.
+__device__ __forceinline__ float sigmoid_fast(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
+
 template <typename TO>
 __device__ __forceinline__ float ld_elem(const void* p, int64_t i) {
   if constexpr (sizeof(TO) == 4) return static_cast<const float*>(p)[i];
@@ -16,12 +35,12 @@ __device__ __forceinline__ float ld_elem(const void* p, int64_t i) {
 template <typename TO>
 __device__ __forceinline__ void st_elem(void* p, int64_t i, float v) {
   if constexpr (sizeof(TO) == 4) static_cast<float*>(p)[i] = v;
-  else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  else static_cast<uint16_t*>(p)[i] = bf16_hw(v);
 }
 template <typename TO>
 __device__ __forceinline__ float round_like(float v) {
   if constexpr (sizeof(TO) == 4) return v;
-  else return bf16_to_f32(f32_to_bf16(v));
+  else return bf16_to_f32(bf16_hw(v));
 }
 
 // a0 = accumulator (gate accumulator in the dual form), a1 = up accumulator.
@@ -36,10 +55,11 @@ __device__ __forceinline__ void epilogue(const GProb& P, int m, int n, float a0,
   } else if constexpr (MODE == EPI_SILU) {
     // gate/up pre-activations leave the accumulator rounded to the path
     // dtype (bf16 in the reference, src/layer_forward_impl.inc:72,122), and
-    // silu(g)*u is formed from those values with the reference's f32 order
-    // (src/kernels_elementwise_impl.inc:440-446): sg = 1/(1+exp(-g)), (g*sg)*u.
+    // silu(g)*u is formed from those values in the reference's f32 order
+    // (src/kernels_elementwise_impl.inc:440-446): sg = 1/(1+exp(-g)), (g*sg)*u,
+    // with sg from sigmoid_fast.
     const float g = round_like<TO>(a0), u = round_like<TO>(a1);
-    const float sg = 1.0f / (1.0f + expf(-g));
+    const float sg = sigmoid_fast(g);
     st_elem<TO>(P.out0, o, g * sg * u);
     if (P.out1) st_elem<TO>(P.out1, o, g);
     if (P.out2) st_elem<TO>(P.out2, o, u);
@@ -48,7 +68,7 @@ __device__ __forceinline__ void epilogue(const GProb& P, int m, int n, float a0,
     // (reference fused_gate_up_bwd_kernel, src/kernels_elementwise_impl.inc:107-117).
     const int64_t oa = (int64_t)m * P.ldaux + n;
     const float g = ld_elem<TO>(P.aux0, oa), u = ld_elem<TO>(P.aux1, oa);
-    const float sg = 1.0f / (1.0f + expf(-g));
+    const float sg = sigmoid_fast(g);
     const float gv = g * sg;
     const float sgrad = sg * (1.0f + g * (1.0f - sg));
     st_elem<TO>(P.out0, o, a0 * u * sgrad);
@@ -166,8 +186,8 @@ __device__ __forceinline__ void unpack8(const u32x4& q, float* f) {
 }
 __device__ __forceinline__ u32x4 pack8(const float* f) {
   u32x4 q;
-  q.x = pack_bf16x2(f[0], f[1]); q.y = pack_bf16x2(f[2], f[3]);
-  q.z = pack_bf16x2(f[4], f[5]); q.w = pack_bf16x2(f[6], f[7]);
+  q.x = pack2_hw(f[0], f[1]); q.y = pack2_hw(f[2], f[3]);
+  q.z = pack2_hw(f[4], f[5]); q.w = pack2_hw(f[6], f[7]);
   return q;
 }
 template <typename TO>
@@ -220,7 +240,7 @@ __device__ __forceinline__ void epi_chunk(const GProb& P, int m, int n, const fl
     for (int j = 0; j < 8; ++j) {
       g[j] = round_like<TO>(v[j]);
       uu[j] = round_like<TO>(u[j]);
-      const float sg = 1.0f / (1.0f + expf(-g[j]));
+      const float sg = sigmoid_fast(g[j]);
       r[j] = g[j] * sg * uu[j];
     }
     st8<TO>(P.out0, o, r);
@@ -233,7 +253,7 @@ __device__ __forceinline__ void epi_chunk(const GProb& P, int m, int n, const fl
     unpack8(uq, uu);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float sg = 1.0f / (1.0f + expf(-g[j]));
+      const float sg = sigmoid_fast(g[j]);
       const float gv = g[j] * sg;
       const float sgrad = sg * (1.0f + g[j] * (1.0f - sg));
       r[j] = v[j] * uu[j] * sgrad;
