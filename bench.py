@@ -43,6 +43,13 @@ GEMM_FLOP = {
     "wgrad": 3 * 2 * S * D * M,     # dW gate/up/down of the slice (one launch)
 }
 STEP_FLOP = sum(GEMM_FLOP.values())
+# algorithmic HBM bytes per launch of the bandwidth-bound kernels
+HBM_BYTES = {
+    "rmsnorm_fwd": 2 * M * D * 2 + D * 2 + M * 4,          # x in, y out (bf16), gamma, mean-square out
+    "rmsnorm_bwd": M * D * (4 + 2 + 4) + D * 2 + M * 4,    # dy f32, x bf16 in, dx f32 out, gamma, mean-square
+    "adamw": S * D * (4 * 4 + 3 * 4),                      # one projection: w, g, m, v in; w, m, v out
+}
+ROPE_B, ROPE_T, ROPE_HQ, ROPE_HK, ROPE_HD, ROPE_THETA = 2, 4096, 32, 8, 128, 500000.0
 
 
 def log(msg):
@@ -57,6 +64,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-bake", action="store_true", help="skip the shadow_bake measurement")
     ap.add_argument("--cpu-tokens", type=int, default=1536)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (scale for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has one GPU); "
@@ -66,6 +75,9 @@ def main():
     import torch
     from glt_amd import _ffi as F, synth
 
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     lib = F.load()
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
@@ -165,6 +177,18 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                 "flop_per_launch": dom_flop}
 
+    # HBM-bound kernels against the HBM roofline: RMSNorm and AdamW of the
+    # step, RoPE at the decoder-layer shape (2 x 4096 tokens, 32 q / 8 kv
+    # heads of 128, theta 5e5)
+    hbm = {}
+    for k, nbytes in (("rmsnorm_fwd", HBM_BYTES["rmsnorm_fwd"]), ("rmsnorm_bwd", HBM_BYTES["rmsnorm_bwd"]),
+                      ("adamw", HBM_BYTES["adamw"])):
+        if k in kernels:
+            t = kernels[k]["avg_ms"]
+            hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
+                      "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+    hbm["rope"] = bench_rope(torch, F, sp, p)
+
     # shadow_bake: 32 layers materialised (config 4)
     bake = None
     if not args.no_bake:
@@ -192,12 +216,51 @@ def main():
         "step_mfma_frac": round(STEP_FLOP / (ms_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "gemm_mfma_frac": round(STEP_FLOP / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "roofline": roofline,
+        "hbm_kernels": hbm,
         "cpu_baseline": cpu,
         "bake": bake,
         "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in sorted(kernels.items())},
     }
     print(json.dumps(out), flush=True)
+
+
+def bench_rope(torch, F, sp, p, reps=20):
+    """RoPE in place on q [2,4096,32*128] and k [2,4096,8*128] bf16 (the
+    decoder-layer shape); algorithmic bytes: q and k read and written."""
+    bf = torch.bfloat16
+    q = torch.empty((ROPE_B, ROPE_T, ROPE_HQ * ROPE_HD), dtype=bf, device="cuda")
+    k = torch.empty((ROPE_B, ROPE_T, ROPE_HK * ROPE_HD), dtype=bf, device="cuda")
+    for i, t in enumerate((q, k)):
+        F.call("glt_fill_normal", p(t), F.DTYPE_BF16, t.numel(), 400, i, 0.0, 1.0, sp)
+
+    def run():
+        F.call("glt_rope_fwd", p(q), ROPE_HQ, p(k), ROPE_HK, ROPE_B, ROPE_T, ROPE_HD, ROPE_THETA, 0, sp)
+
+    run()
+    torch.cuda.synchronize()
+    F.call("glt_profile_enable", 1)
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    tot, cnt = F.profile_collect().get("rope", (0.0, 1))
+    F.call("glt_profile_enable", 0)
+    t = tot / cnt
+    nbytes = 2 * 2 * ROPE_B * ROPE_T * (ROPE_HQ + ROPE_HK) * ROPE_HD
+    return {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+
+def calibrate_copy(torch, nbytes=1 << 30, reps=3):
+    """A plain device-to-device copy of nbytes, reps times: the reference
+    kernel whose FETCH_SIZE / WRITE_SIZE (known to be nbytes each) scales
+    the counter readings of the path's kernels."""
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes": nbytes, "reps": reps}), flush=True)
 
 
 def bench_bake(torch, F, lib, dev, sp, p, L=32, reps=5):
