@@ -188,6 +188,7 @@ def main():
             hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
                       "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
     hbm["rope"] = bench_rope(torch, F, sp, p)
+    hbm["torch_copy"] = bench_copy(torch)
 
     # shadow_bake: 32 layers materialised (config 4)
     bake = None
@@ -249,6 +250,27 @@ def bench_rope(torch, F, sp, p, reps=20):
     nbytes = 2 * 2 * ROPE_B * ROPE_T * (ROPE_HQ + ROPE_HK) * ROPE_HD
     return {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+
+def bench_copy(torch, nbytes=1 << 30, reps=10):
+    """Device-to-device copy of 1 GiB with torch's copy kernel (bytes = read
+    + write), reported beside the HBM-bound kernels as a familiar yardstick;
+    it is not the hardware ceiling (a one-16-byte-chunk-per-thread
+    nontemporal copy streams faster)."""
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / reps
+    del src, dst
+    return {"bytes": 2 * nbytes, "ms": round(t, 5), "GB_per_s": round(2 * nbytes / (t * 1e-3) / 1e9, 1),
+            "frac_hbm": round(2 * nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
 
 
 def calibrate_copy(torch, nbytes=1 << 30, reps=3):

@@ -4,12 +4,21 @@
 // rounding as the reference kernel (src/shadow_bake_impl.inc:46-49), so the
 // result is bit-exact. The reference launches one workgroup per graft row
 // and, for the down projection, writes the transposed block with a row
-// stride of I elements per lane (uncoalesced). Here a workgroup owns a 64x64
-// output tile: the base part streams through 16-byte loads/stores, and the
-// graft part of the tile is staged through LDS in output orientation, so the
-// down projection's transpose is read coalesced along the graft's contiguous
-// axis. One launch covers up to kMaxLayers layers (grid.z), so a 32-layer
-// bake is three launches instead of 96.
+// stride of I elements per lane (uncoalesced).
+//
+// Here one launch covers up to kMaxLayers layers (grid.z) and has two kinds
+// of workgroup:
+//  * stream blocks: each thread owns one 16-byte chunk (8 elements) of an
+//    output row, consecutive threads and workgroups walk consecutive chunks
+//    of the row-major region, so HBM sees long sequential runs in both the
+//    base read and the output write. Gate/up graft rows are contiguous along
+//    the output row, so they are added straight from global memory.
+//  * tile blocks (down projection only): a 64x64 output tile that a graft
+//    block touches. The graft's contiguous axis runs down the output column,
+//    so the tile stages it through LDS and adds it in output orientation.
+//    Stream blocks skip every chunk of such a tile.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace glt {
@@ -32,6 +41,9 @@ struct BakeLaunch {
   int src_rows, src_cols;    // base extent; reads outside are zero (appended tail)
   int64_t src_ld, dst_ld;
   int reg_r0, reg_r1, reg_c0, reg_c1;  // output region processed
+  int chunks_per_row;        // 8-element chunks per region row
+  uint32_t stream_chunks;    // chunks per layer handled by stream blocks
+  int tile_bx0, tile_by0, tiles_x, n_tile_blocks;  // tile blocks: bounding box in region tile units
 };
 
 template <typename G>
@@ -41,55 +53,139 @@ template <> __device__ __forceinline__ float gload<uint16_t>(const uint16_t* p, 
   return bf16_to_f32(p[i]);
 }
 
-template <typename G>
-__global__ void __launch_bounds__(256) bake_tile_kernel(const BakeLaunch a) {
-  __shared__ float gt[kTile][kTile + 1];
-  const int L = blockIdx.z;
-  const int tr0 = a.reg_r0 + blockIdx.y * kTile;
-  const int tc0 = a.reg_c0 + blockIdx.x * kTile;
-  const int tr1 = min(tr0 + kTile, a.reg_r1);
-  const int tc1 = min(tc0 + kTile, a.reg_c1);
-  const int t = threadIdx.x;
+// 8 consecutive graft values from a 16-byte aligned address.
+__device__ __forceinline__ void gload8(const float* p, float* v) {
+  const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + 1);
+  v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+  v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+}
+__device__ __forceinline__ void unpack8(const u32x4 q, float* v) {
+  v[0] = bf16_to_f32((uint16_t)(q.x & 0xFFFF)); v[1] = bf16_to_f32((uint16_t)(q.x >> 16));
+  v[2] = bf16_to_f32((uint16_t)(q.y & 0xFFFF)); v[3] = bf16_to_f32((uint16_t)(q.y >> 16));
+  v[4] = bf16_to_f32((uint16_t)(q.z & 0xFFFF)); v[5] = bf16_to_f32((uint16_t)(q.z >> 16));
+  v[6] = bf16_to_f32((uint16_t)(q.w & 0xFFFF)); v[7] = bf16_to_f32((uint16_t)(q.w >> 16));
+}
+__device__ __forceinline__ void gload8(const uint16_t* p, float* v) {
+  unpack8(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)), v);
+}
 
-  // Which slices touch this tile (block-uniform).
+// Does any slice's block (in output orientation) intersect the tile at
+// (tr0, tc0)? Block-uniform.
+__device__ __forceinline__ bool tile_hit(const BakeLaunch& a, int tr0, int tc0) {
+  const int tr1 = min(tr0 + kTile, a.reg_r1), tc1 = min(tc0 + kTile, a.reg_c1);
   bool any = false;
-  for (int j = 0; j < a.nslices; ++j) {
+#pragma unroll
+  for (int j = 0; j < kMaxBakeSlices; ++j) {
+    if (j >= a.nslices) break;
     const BakePlacement p = a.pl[j];
     const int fr0 = a.trans ? p.h0 : p.i0, fr1 = a.trans ? p.h0 + p.h : p.i0 + p.s;
     const int fc0 = a.trans ? p.i0 : p.h0, fc1 = a.trans ? p.i0 + p.s : p.h0 + p.h;
     any |= (max(tr0, fr0) < min(tr1, fr1)) && (max(tc0, fc0) < min(tc1, fc1));
   }
-  if (any) {
+  return any;
+}
+
+// Base chunk (r, c..c+7) as f32; elements outside the base extent or past
+// c_end read zero.
+__device__ __forceinline__ void load_base8(const BakeLaunch& a, const uint16_t* src, int r, int c, int c_end,
+                                           float* v) {
+  const bool in_rows = r < a.src_rows;
+  const int64_t so = (int64_t)r * a.src_ld + c;
+  if (in_rows && c + 8 <= a.src_cols && c + 8 <= c_end && ((reinterpret_cast<uintptr_t>(src + so) & 15) == 0)) {
+    unpack8(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + so)), v);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (in_rows && c + j < a.src_cols && c + j < c_end) ? bf16_to_f32(src[so + j]) : 0.f;
+  }
+}
+
+__device__ __forceinline__ void store8(uint16_t* dst, int64_t dofs, int c, int c_end, const float* v) {
+  if (c + 8 <= c_end && ((reinterpret_cast<uintptr_t>(dst + dofs) & 15) == 0)) {
+    u32x4 o;
+    o.x = pack_bf16x2(v[0], v[1]);
+    o.y = pack_bf16x2(v[2], v[3]);
+    o.z = pack_bf16x2(v[4], v[5]);
+    o.w = pack_bf16x2(v[6], v[7]);
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst + dofs));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (c + j < c_end) dst[dofs + j] = f32_to_bf16(v[j]);
+  }
+}
+
+template <typename G>
+__device__ __forceinline__ void bake_stream(const BakeLaunch& a, int L, uint32_t q) {
+  if (q >= a.stream_chunks) return;
+  const uint32_t cpr = (uint32_t)a.chunks_per_row;
+  const uint32_t qr = q / cpr;
+  const int r = a.reg_r0 + (int)qr, c = a.reg_c0 + 8 * (int)(q - qr * cpr);
+  // chunks are 8-aligned from reg_c0, so a chunk lies in exactly one tile
+  if (a.n_tile_blocks && tile_hit(a, a.reg_r0 + ((r - a.reg_r0) & ~(kTile - 1)),
+                                  a.reg_c0 + ((c - a.reg_c0) & ~(kTile - 1))))
+    return;
+  const int c_end = min(c + 8, a.reg_c1);
+  float v[8];
+  load_base8(a, a.src[L], r, c, c_end, v);
+  if (!a.trans) {
     // -0.0 is the additive identity for every f32 (x + -0.0 == x, also for
-    // x = -0.0), so tile elements no slice covers pass the base through bit
-    // for bit; a covered element becomes base + delta.
-    for (int e = t; e < kTile * kTile; e += 256) gt[e >> 6][e & 63] = -0.0f;
-    __syncthreads();
-    for (int j = 0; j < a.nslices; ++j) {
+    // x = -0.0), so elements no slice covers pass the base through bit for
+    // bit; a covered element becomes base + delta. The tile blocks sum the
+    // same way.
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = -0.0f;
+    bool hit = false;
+#pragma unroll
+    for (int j = 0; j < kMaxBakeSlices; ++j) {
+      if (j >= a.nslices) break;
       const BakePlacement p = a.pl[j];
-      const G* g = static_cast<const G*>(a.graft[L][j]);
-      if (!g) continue;
-      if (!a.trans) {
-        // out(r, c) += G[r - i0, c - h0]; consecutive threads walk c (contiguous in G)
-        for (int e = t; e < kTile * kTile; e += 256) {
-          const int lr = e >> 6, lc = e & 63, r = tr0 + lr, c = tc0 + lc;
-          if (r < tr1 && c < tc1 && r >= p.i0 && r < p.i0 + p.s && c >= p.h0 && c < p.h0 + p.h)
-            gt[lr][lc] += gload(g, (int64_t)(r - p.i0) * p.h + (c - p.h0));
-        }
+      if (r < p.i0 || r >= p.i0 + p.s) continue;
+      const int lo = max(c, p.h0), hi = min(c_end, p.h0 + p.h);
+      if (lo >= hi) continue;
+      hit = true;
+      const G* g = static_cast<const G*>(a.graft[L][j]) + (int64_t)(r - p.i0) * p.h + (c - p.h0);
+      if (lo == c && hi == c + 8 && ((reinterpret_cast<uintptr_t>(g) & 15) == 0)) {
+        float w[8];
+        gload8(g, w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += w[e];
       } else {
-        // out(r, c) += G[c - i0, r - h0]; consecutive threads walk r (contiguous in G)
-        for (int e = t; e < kTile * kTile; e += 256) {
-          const int lc = e >> 6, lr = e & 63, r = tr0 + lr, c = tc0 + lc;
-          if (r < tr1 && c < tc1 && c >= p.i0 && c < p.i0 + p.s && r >= p.h0 && r < p.h0 + p.h)
-            gt[lr][lc] += gload(g, (int64_t)(c - p.i0) * p.h + (r - p.h0));
-        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (c + e >= lo && c + e < hi) acc[e] += gload(g, e);
       }
     }
-    __syncthreads();
+    if (hit) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += acc[e];
+    }
   }
+  store8(a.dst[L], (int64_t)r * a.dst_ld + c, c, c_end, v);
+}
 
-  const uint16_t* src = a.src[L];
-  uint16_t* dst = a.dst[L];
+template <typename G>
+__device__ __forceinline__ void bake_tile(const BakeLaunch& a, int L, int tb, float (*gt)[kTile + 1]) {
+  const int tr0 = a.reg_r0 + (a.tile_by0 + tb / a.tiles_x) * kTile;
+  const int tc0 = a.reg_c0 + (a.tile_bx0 + tb % a.tiles_x) * kTile;
+  if (!tile_hit(a, tr0, tc0)) return;  // stream blocks cover it
+  const int tr1 = min(tr0 + kTile, a.reg_r1);
+  const int tc1 = min(tc0 + kTile, a.reg_c1);
+  const int t = threadIdx.x;
+  for (int e = t; e < kTile * kTile; e += 256) gt[e >> 6][e & 63] = -0.0f;
+  __syncthreads();
+  for (int j = 0; j < a.nslices; ++j) {
+    const BakePlacement p = a.pl[j];
+    const G* g = static_cast<const G*>(a.graft[L][j]);
+    // out(r, c) += G[c - i0, r - h0]; consecutive threads walk r (contiguous in G)
+    for (int e = t; e < kTile * kTile; e += 256) {
+      const int lc = e >> 6, lr = e & 63, r = tr0 + lr, c = tc0 + lc;
+      if (r < tr1 && c < tc1 && c >= p.i0 && c < p.i0 + p.s && r >= p.h0 && r < p.h0 + p.h)
+        gt[lr][lc] += gload(g, (int64_t)(c - p.i0) * p.h + (r - p.h0));
+    }
+  }
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int q = t + 256 * i;
@@ -97,49 +193,67 @@ __global__ void __launch_bounds__(256) bake_tile_kernel(const BakeLaunch a) {
     const int r = tr0 + lr, c = tc0 + lc;
     if (r >= tr1 || c >= tc1) continue;
     float v[8];
-    const bool in_rows = r < a.src_rows;
-    const int64_t so = (int64_t)r * a.src_ld + c;
-    const bool vec_src = in_rows && c + 8 <= a.src_cols && ((reinterpret_cast<uintptr_t>(src + so) & 15) == 0);
-    if (vec_src) {
-      const u32x4 qv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + so));
-      v[0] = bf16_to_f32((uint16_t)(qv.x & 0xFFFF)); v[1] = bf16_to_f32((uint16_t)(qv.x >> 16));
-      v[2] = bf16_to_f32((uint16_t)(qv.y & 0xFFFF)); v[3] = bf16_to_f32((uint16_t)(qv.y >> 16));
-      v[4] = bf16_to_f32((uint16_t)(qv.z & 0xFFFF)); v[5] = bf16_to_f32((uint16_t)(qv.z >> 16));
-      v[6] = bf16_to_f32((uint16_t)(qv.w & 0xFFFF)); v[7] = bf16_to_f32((uint16_t)(qv.w >> 16));
-    } else {
+    load_base8(a, a.src[L], r, c, tc1, v);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        v[j] = (in_rows && c + j < a.src_cols && c + j < tc1) ? bf16_to_f32(src[so + j]) : 0.f;
-    }
-    if (any) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] += gt[lr][lc + j];
-    }
-    const int64_t dofs = (int64_t)r * a.dst_ld + c;
-    if (c + 8 <= tc1 && ((reinterpret_cast<uintptr_t>(dst + dofs) & 15) == 0)) {
-      u32x4 o;
-      o.x = pack_bf16x2(v[0], v[1]);
-      o.y = pack_bf16x2(v[2], v[3]);
-      o.z = pack_bf16x2(v[4], v[5]);
-      o.w = pack_bf16x2(v[6], v[7]);
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dst + dofs));
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (c + j < tc1) dst[dofs + j] = f32_to_bf16(v[j]);
-    }
+    for (int j = 0; j < 8; ++j) v[j] += gt[lr][lc + j];
+    store8(a.dst[L], (int64_t)r * a.dst_ld + c, c, tc1, v);
   }
 }
 
+template <typename G>
+__global__ void __launch_bounds__(256) bake_kernel(const BakeLaunch a) {
+  __shared__ float gt[kTile][kTile + 1];
+  const int L = blockIdx.z;
+  if ((int)blockIdx.x < a.n_tile_blocks)
+    bake_tile<G>(a, L, blockIdx.x, gt);
+  else
+    bake_stream<G>(a, L, (uint32_t)(blockIdx.x - a.n_tile_blocks) * 256u + threadIdx.x);
+}
+
+// Fills the work split of a launch whose region, slices and orientation are
+// set, then launches it over `nlayers` layers.
 static glt_status launch_bake(BakeLaunch& a, int nlayers, int graft_dtype, hipStream_t st) {
   if (nlayers == 0 || a.reg_r1 <= a.reg_r0 || a.reg_c1 <= a.reg_c0) return GLT_OK;
-  dim3 grid((unsigned)cdiv(a.reg_c1 - a.reg_c0, kTile), (unsigned)cdiv(a.reg_r1 - a.reg_r0, kTile),
-            (unsigned)nlayers);
+  const int rows = a.reg_r1 - a.reg_r0, cols = a.reg_c1 - a.reg_c0;
+  a.chunks_per_row = cdiv(cols, 8);
+  const int64_t chunks = (int64_t)rows * a.chunks_per_row;
+  GLT_CHECK(chunks < (int64_t)UINT32_MAX - 256, GLT_ERR_SHAPE, "shadow_bake: %d x %d region too large", rows,
+            cols);
+  a.stream_chunks = (uint32_t)chunks;
+  a.n_tile_blocks = 0;
+  a.tiles_x = 1;
+  a.tile_bx0 = a.tile_by0 = 0;
+  if (a.trans) {
+    // bounding box, in region tile units, of the tiles the slices touch
+    int bx0 = INT32_MAX, by0 = INT32_MAX, bx1 = -1, by1 = -1;
+    bool whole = false;
+    for (int j = 0; j < a.nslices; ++j) {
+      const BakePlacement p = a.pl[j];
+      const int r0 = std::max(p.h0, a.reg_r0), r1 = std::min(p.h0 + p.h, a.reg_r1);
+      const int c0 = std::max(p.i0, a.reg_c0), c1 = std::min(p.i0 + p.s, a.reg_c1);
+      if (r0 >= r1 || c0 >= c1) continue;
+      by0 = std::min(by0, (r0 - a.reg_r0) / kTile);
+      by1 = std::max(by1, (r1 - 1 - a.reg_r0) / kTile);
+      bx0 = std::min(bx0, (c0 - a.reg_c0) / kTile);
+      bx1 = std::max(bx1, (c1 - 1 - a.reg_c0) / kTile);
+      whole |= r0 == a.reg_r0 && r1 == a.reg_r1 && c0 == a.reg_c0 && c1 == a.reg_c1;
+    }
+    if (bx1 >= 0) {
+      a.tile_bx0 = bx0;
+      a.tile_by0 = by0;
+      a.tiles_x = bx1 - bx0 + 1;
+      a.n_tile_blocks = a.tiles_x * (by1 - by0 + 1);
+      // one slice covering the whole region: every chunk is in a tile
+      if (whole) a.stream_chunks = 0;
+    }
+  }
+  const int64_t blocks = a.n_tile_blocks + cdiv((int64_t)a.stream_chunks, 256);
+  dim3 grid((unsigned)blocks, 1, (unsigned)nlayers);
   if (graft_dtype == GLT_DTYPE_F32)
-    GLT_LAUNCH("bake", bake_tile_kernel<float>, grid, dim3(256), 0, st, a);
+    GLT_LAUNCH("bake", bake_kernel<float>, grid, dim3(256), 0, st, a);
   else
-    GLT_LAUNCH("bake", bake_tile_kernel<uint16_t>, grid, dim3(256), 0, st, a);
-  GLT_LAUNCH_CHECK("bake_tile");
+    GLT_LAUNCH("bake", bake_kernel<uint16_t>, grid, dim3(256), 0, st, a);
+  GLT_LAUNCH_CHECK("bake");
   return GLT_OK;
 }
 

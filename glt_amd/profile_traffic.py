@@ -28,7 +28,7 @@ KERNELS = {
     "rmsnorm_bwd": ("rmsnorm_bwd", None),
     "adamw": ("adamw_kernel", None),
     "rope": ("rope_kernel", None),
-    "bake": ("bake_tile_kernel", None),
+    "bake": ("bake_kernel", None),
 }
 
 
