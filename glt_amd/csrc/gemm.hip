@@ -124,17 +124,17 @@ __device__ __forceinline__ bool seg_hits(const GSeg& S, const GProb& P, int n0, 
 // loads, issued one K-step ahead. Rows outside a tile's valid range get an
 // out-of-range offset and arrive as zeros. The load side walks the K-steps
 // of all of the workgroup's tiles as one stream, so the next tile's first
-// steps are in flight while the epilogue of the current one runs; the
-// epilogue stages accumulators through a separate 32 KB area, private per
-// wavefront.
+// steps are in flight while the epilogue of the current one runs. The
+// epilogue stores straight from the accumulators: the MFMA takes the B
+// fragment as its first operand, which leaves each lane four consecutive
+// output columns of one row per accumulator group.
 // =========================================================================
 constexpr int kBM = 256, kBK = 64;
 constexpr int kTileElems = kBM * kBK;                    // one A tile = one LDS stage (32 KB)
 constexpr int kAStages = 4;
 constexpr uint32_t kExtent = 0x7FFFFFF0u;                // buffer extent below kOob
-constexpr int kEpRows = 16;                              // rows per staged half-band
-constexpr int kEpWaveWords = kEpRows * 128;              // f32 staging words per wavefront
-constexpr size_t kMfmaLds = ((size_t)kAStages * kTileElems * 2) + 4 * kEpWaveWords * 4;  // 160 KB
+constexpr int kEpWaveBytes = 8192;                         // epilogue staging per wavefront
+constexpr size_t kMfmaLds = (size_t)kAStages * kTileElems * 2 + 4 * kEpWaveBytes;  // 160 KB
 constexpr uint32_t kShufStepBytes = kShufBlock * 2;      // one 32 x 64 block of B (4 KB)
 
 // Rows are 64 bf16 = 128 bytes, one cache line each, so every global
@@ -144,15 +144,6 @@ constexpr uint32_t kShufStepBytes = kShufBlock * 2;      // one 32 x 64 block of
 // bank group 8*(row&1) + physical chunk, so the physical chunk is the
 // logical one XOR (row>>1)&7, which makes the 16 groups distinct.
 __device__ __forceinline__ int swz_key(int row) { return (row >> 1) & 7; }
-
-// Epilogue staging layout: row-major 16 x 128 f32 per wavefront, column
-// XOR-swizzled so that (a) the accumulator writes, where lanes 0-31 and
-// 32-63 fill rows four apart, hit all 64 banks (bit 5 follows row bit 2) and
-// (b) the 16-byte row reads of 16 lanes, which cover 128 columns, split over
-// both bank halves (bit 2 follows column bit 6 and row bit 0).
-__device__ __forceinline__ int ep_col(int row, int col) {
-  return col ^ (((row >> 2) & 1) << 5) ^ ((((col >> 6) ^ row) & 1) << 2);
-}
 
 // Buffer descriptor of a wave-uniform base and extent. The compiler loses
 // track of their uniformity through the kernel's position bookkeeping and
@@ -169,6 +160,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uni_rsrc(const void* p, uint32
 // expcnt / lgkmcnt unconstrained.
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 // Orders one wavefront's LDS accesses across lanes: LDS executes a
 // wavefront's instructions in order, so only the compiler must not move
 // accesses across this point.
@@ -178,90 +171,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ void unpack8(const u32x4& q, float* f) {
-  f[0] = bf16_to_f32((uint16_t)(q.x & 0xFFFF)); f[1] = bf16_to_f32((uint16_t)(q.x >> 16));
-  f[2] = bf16_to_f32((uint16_t)(q.y & 0xFFFF)); f[3] = bf16_to_f32((uint16_t)(q.y >> 16));
-  f[4] = bf16_to_f32((uint16_t)(q.z & 0xFFFF)); f[5] = bf16_to_f32((uint16_t)(q.z >> 16));
-  f[6] = bf16_to_f32((uint16_t)(q.w & 0xFFFF)); f[7] = bf16_to_f32((uint16_t)(q.w >> 16));
-}
-__device__ __forceinline__ u32x4 pack8(const float* f) {
-  u32x4 q;
-  q.x = pack2_hw(f[0], f[1]); q.y = pack2_hw(f[2], f[3]);
-  q.z = pack2_hw(f[4], f[5]); q.w = pack2_hw(f[6], f[7]);
-  return q;
-}
-template <typename TO>
-__device__ __forceinline__ void ld8(const void* p, int64_t o, float* f) {
-  if constexpr (sizeof(TO) == 4) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + o);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + o + 4);
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-  } else {
-    unpack8(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p) + o), f);
-  }
-}
-template <typename TO>
-__device__ __forceinline__ void st8(void* p, int64_t o, const float* f) {
-  if constexpr (sizeof(TO) == 4) {
-    float* q = static_cast<float*>(p) + o;
-    *reinterpret_cast<f32x4*>(q) = f32x4{f[0], f[1], f[2], f[3]};
-    *reinterpret_cast<f32x4*>(q + 4) = f32x4{f[4], f[5], f[6], f[7]};
-  } else {
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p) + o) = pack8(f);
-  }
-}
-
-// Eight consecutive output columns n..n+7 of row m (v = accumulators; u =
-// up accumulators in the dual form; gq/uq = the saved bf16 gate/up
-// pre-activations of these columns for EPI_DGDU, loaded ahead). Vector path
-// when the chunk is whole; outputs and aux rows are 16-byte aligned
-// (checked on the host).
-template <typename TO, int MODE>
-__device__ __forceinline__ void epi_chunk(const GProb& P, int m, int n, const float* v, const float* u,
-                                          const u32x4& gq, const u32x4& uq) {
-  if (m >= P.M) return;
-  if (n + 8 > P.N) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)  // unrolled: v and u live in registers
-      if (n + j < P.N) epilogue<TO, MODE>(P, m, n + j, v[j], u[j]);
-    return;
-  }
-  const int64_t o = (int64_t)m * P.ldo + n;
-  float r[8];
-  if constexpr (MODE == EPI_STORE) {
-    float old[8];
-    if (P.beta != 0.f) ld8<TO>(P.out0, o, old);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = P.alpha * v[j] + (P.beta != 0.f ? P.beta * old[j] : 0.f);
-    st8<TO>(P.out0, o, r);
-  } else if constexpr (MODE == EPI_SILU) {
-    float g[8], uu[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      g[j] = round_like<TO>(v[j]);
-      uu[j] = round_like<TO>(u[j]);
-      const float sg = sigmoid_fast(g[j]);
-      r[j] = g[j] * sg * uu[j];
-    }
-    st8<TO>(P.out0, o, r);
-    if (P.out1) st8<TO>(P.out1, o, g);
-    if (P.out2) st8<TO>(P.out2, o, uu);
-  } else {
-    static_assert(MODE != EPI_DGDU || sizeof(TO) == 2, "the staged DGDU epilogue reads bf16 aux");
-    float g[8], uu[8], du[8];
-    unpack8(gq, g);
-    unpack8(uq, uu);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float sg = sigmoid_fast(g[j]);
-      const float gv = g[j] * sg;
-      const float sgrad = sg * (1.0f + g[j] * (1.0f - sg));
-      r[j] = v[j] * uu[j] * sgrad;
-      du[j] = v[j] * gv;
-    }
-    st8<TO>(P.out0, o, r);
-    st8<TO>(P.out1, o, du);
-  }
+// One accumulator element moved to a VGPR where it is used. Arithmetic
+// cannot read AGPRs; left to itself the compiler copies every accumulator
+// to VGPRs as the K loop exits (256 registers at once) and spills. The
+// "a" operand keeps the accumulators in AGPRs up to each group's reads.
+__device__ __forceinline__ float acc_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
 }
 
 template <typename TO, int MODE, bool DUAL>
@@ -426,7 +343,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[fs][i], fb[s][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[s][j], fa[fs][i], acc[i][j], 0, 0, 0);
       read_a(rst, rks, fs ^ 1, j);
       load_b(s, j);
       extra(j);
@@ -463,8 +380,10 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   for (int i = 0; i < 4; ++i) read_a(0, 0, 0, i);
   int g = 0;  // K-steps consumed so far; step g's A tile sits in stage g % 4
 
-  float* ep = reinterpret_cast<float*>(smem + kAStages * kTileElems) + wave * kEpWaveWords;
-  const int cr = 4 * (lane >> 5), cc = lane & 31;
+  char* const ep = reinterpret_cast<char*>(smem) + (size_t)kAStages * kTileElems * 2 + wave * kEpWaveBytes;
+  // A of the step after the current one is already known to have landed
+  // (waited for before the last epilogue)
+  bool prewaited = false;
   for (int ct = first; ct < total; ct += G) {
     int tm, tn;
     const int pi = locate_tile(args, ct, tm, tn);
@@ -492,15 +411,20 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
       phase(0, 0, st, 1, no_extra);
       phase(1, 1, st, 2, no_extra);
       phase(0, 2, st, 3, no_extra);
-      // Loads issued after this thread's A loads of step g+1 (the A loads
-      // of steps g+2, g+3 and the B loads in between): 44 in step 0 and 60
-      // in step 1 (the fill order), at least 64 later. Loads complete in
-      // order, so vmcnt <= n with n at most that count means step g+1 has
-      // landed. (Epilogue stores in between may complete in any order; they
-      // only raise the count.)
-      if (g >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(63));
-      else if (g == 1) __builtin_amdgcn_s_waitcnt(vmcnt_enc(60));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_enc(44));
+      // Loads complete in order, so vmcnt <= n guarantees every load that
+      // has at least n loads issued after it. After the last A load of step
+      // g+1 come 44 loads in step 0 (the fill order) and, from step 1 on,
+      // 60: two whole steps (16 B + 8 A each) and the 12 B loads of phases
+      // 0-2. Stores in between only raise the count. Right after an
+      // epilogue that wait was already done before it, with no stores
+      // outstanding.
+      if (prewaited) {
+      } else if (g == 0) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(44));
+      } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(60));
+      }
+      prewaited = false;
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
       phase(1, 3, nst, 0, [&](int j) {
@@ -510,91 +434,203 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
       adv_a();
       adv_b();
     }
+    // The first step of the next tile needs A of step g+1 (g = steps
+    // consumed). Once a step has run, its last load has at least 48 loads
+    // after it (the two steps since), so waiting here, before the
+    // epilogue's stores raise the count, is nearly free. (With no step run
+    // yet only 32 follow it; the first step then waits as usual.)
+    __builtin_amdgcn_s_waitcnt(vmcnt_enc(48));
+    prewaited = g > 0;
 
-    // ---- epilogue, per 16-row half-band: accumulators -> private LDS
-    // block -> row-wise reads so every lane handles 8 consecutive columns
-    // with 16-byte loads/stores. A tile without K-steps has zero
-    // accumulators and skips the staging.
+    // ---- epilogue. The B fragment is the MFMA's first operand, so block
+    // acc[i][j] is the transposed 32x32 product: lane l owns output row
+    // 32*i + (l & 31) of the wavefront's rows and, in elements 4q..4q+3, the
+    // four consecutive columns 32*jc + 8*q + 4*(l >> 5) .. +3 of its columns
+    // (jc = j; dual: j & 1, with j < 2 gate and j >= 2 up). Groups of four
+    // go to the wavefront's private LDS block as one 8-byte (bf16) or
+    // 16-byte (f32) write and come back row-wise, so each global access is
+    // 16 bytes per lane over whole 128-byte lines.
+    constexpr int ESZ = sizeof(TO);
     const int rbase = m0 + wm * 128;
-    __amdgpu_buffer_rsrc_t rG, rU;
-    u32x4 gq[2][4], uq[2][4];
-    auto prefetch = [&](int i, int hh) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = rbase + i * 32 + hh * 16 + (lane >> 4) + 4 * q;
-        const int n = n0 + wn * 128 + (lane & 15) * 8;
-        const uint32_t off = (m < P.M && n + 8 <= P.N) ? (uint32_t)(((int64_t)m * P.ldaux + n) * 2) : kOob;
-        gq[hh][q] = buf_load16(rG, off);
-        uq[hh][q] = buf_load16(rU, off);
-      }
+    const int cbase = n0 + (DUAL ? wn * 64 : wn * 128);
+    const int wr = lane & 31, wh = lane >> 5;  // staging-write row and half
+    const __amdgpu_buffer_rsrc_t r0 = uni_rsrc(P.out0, kExtent);
+    // byte offset of output (row, col), kOob outside [M, N)
+    auto ooff = [&](int row, int col, int64_t ld, int esz) {
+      return (row < P.M && col < P.N) ? (uint32_t)(((int64_t)row * ld + col) * esz) : kOob;
     };
-    if constexpr (MODE == EPI_DGDU) {
-      rG = make_rsrc(P.aux0, kExtent);
-      rU = make_rsrc(P.aux1, kExtent);
-    }
-    auto stage_half = [&](const f32x16* a, int e0) {
+    if constexpr (ESZ == 2 && MODE != EPI_DGDU) {
+      // bf16 outputs. Plain: 32 rows x 128 columns per block (256-byte
+      // rows, 16 chunks); dual: 32 x 64 per output (128-byte rows, 8
+      // chunks). Chunk c of row r sits at chunk c ^ key(r) and its two
+      // 8-byte halves swap for r >= 16: the 32 rows of one 8-byte write
+      // then cover all 64 banks once, and so do the 16-byte row reads.
+      constexpr int kPitch = DUAL ? 128 : 256;
+      auto key = [](int r) { return DUAL ? (r >> 1) & 7 : r & 15; };
+      auto put = [&](int c, u32x2 d) {
+        *reinterpret_cast<u32x2*>(ep + wr * kPitch + ((c ^ key(wr)) << 4) + ((wh ^ (wr >> 4)) << 3)) = d;
+      };
+      // reads: DUAL 8 lanes x 8 rows per instruction, plain 16 x 4
+      constexpr int kLanesPerRow = kPitch / 16, kRowsPerRead = 64 / kLanesPerRow;
+      const int rc = lane % kLanesPerRow, rr0 = lane / kLanesPerRow;
+      auto drain = [&](__amdgpu_buffer_rsrc_t r, int i) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int row = 8 * (e >> 2) + cr + (e & 3);
-          ep[row * 128 + ep_col(row, j * 32 + cc)] = a[j][e0 + e];
+        for (int k = 0; k < 32 / kRowsPerRead; ++k) {
+          const int row = k * kRowsPerRead + rr0;
+          u32x4 q = *reinterpret_cast<const u32x4*>(ep + row * kPitch + ((rc ^ key(row)) << 4));
+          if (k * kRowsPerRead >= 16) q = u32x4{q.z, q.w, q.x, q.y};
+          __builtin_amdgcn_raw_buffer_store_b128(q, r, ooff(rbase + 32 * i + row, cbase + 8 * rc, P.ldo, 2), 0, 0);
         }
-    };
-    auto read8 = [&](int row, int col, float* v) {
-      if (T == 0) {
+      };
+      if constexpr (MODE == EPI_STORE) {
+        const float alpha = P.alpha;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = 0.f;
-        return;
-      }
-      const float* p = ep + row * 128;
-      const int c0 = ep_col(row, col);
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(p + c0);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(p + (c0 ^ 4));
-      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w; v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-    };
-    // The band loop stays rolled (the chunk code is large); the switch keeps
-    // every accumulator access compile-time indexed, i.e. in registers.
-#pragma unroll 1
-    for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        // this half-band's aux rows, in flight while its accumulators are
-        // staged (a look-ahead would need more registers than remain)
-        if constexpr (MODE == EPI_DGDU) prefetch(i, hh);
-        if (T > 0) {
-          switch (i) {
-            case 0: stage_half(acc[0], hh * 8); break;
-            case 1: stage_half(acc[1], hh * 8); break;
-            case 2: stage_half(acc[2], hh * 8); break;
-            default: stage_half(acc[3], hh * 8); break;
-          }
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float v[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = alpha * acc_read(acc[i][j][4 * q + e]);
+              put(4 * j + q, u32x2{pack2_hw(v[0], v[1]), pack2_hw(v[2], v[3])});
+            }
+          wave_lds_sync();
+          drain(r0, i);
+          wave_lds_sync();
         }
-        wave_lds_sync();
-        const int row0 = rbase + i * 32 + hh * 16;
-        if constexpr (DUAL) {
-          // columns [0,64) of the block hold gate, [64,128) up, same output columns
+      } else {
+        // gate/up pre-activations leave the accumulator rounded to the path
+        // dtype; silu(g)*u is formed from those values. A null out1/out2
+        // gets a zero-extent descriptor, whose stores are dropped.
+        const __amdgpu_buffer_rsrc_t r1 = uni_rsrc(P.out1, P.out1 ? kExtent : 0u);
+        const __amdgpu_buffer_rsrc_t r2 = uni_rsrc(P.out2, P.out2 ? kExtent : 0u);
 #pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const int r = (lane >> 3) + 8 * q, c8 = (lane & 7) * 8;
-            float v[8], u[8];
-            read8(r, c8, v);
-            read8(r, 64 + c8, u);
-            epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 64 + c8, v, u, gq[0][0], uq[0][0]);
-          }
-        } else {
+        for (int i = 0; i < 4; ++i) {
+          u32x2 pg[2][4], pu[2][4];
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float g[4], u[4], r[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                g[e] = round_like<TO>(acc_read(acc[i][j][4 * q + e]));
+                u[e] = round_like<TO>(acc_read(acc[i][j + 2][4 * q + e]));
+                r[e] = g[e] * sigmoid_fast(g[e]) * u[e];
+              }
+              pg[j][q] = u32x2{pack2_hw(g[0], g[1]), pack2_hw(g[2], g[3])};
+              pu[j][q] = u32x2{pack2_hw(u[0], u[1]), pack2_hw(u[2], u[3])};
+              put(4 * j + q, u32x2{pack2_hw(r[0], r[1]), pack2_hw(r[2], r[3])});
+            }
+          wave_lds_sync();
+          drain(r0, i);
+          wave_lds_sync();
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) put(4 * j + q, pg[j][q]);
+          wave_lds_sync();
+          drain(r1, i);
+          wave_lds_sync();
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) put(4 * j + q, pu[j][q]);
+          wave_lds_sync();
+          drain(r2, i);
+          wave_lds_sync();
+        }
+      }
+    } else {
+      // f32 staging: each block is done in two halves of 32 rows x 64
+      // columns (256-byte rows, 16 chunks of four f32; chunk c of row r at
+      // c ^ (r & 15)). A write puts 16 lanes on 16 rows of one chunk, a
+      // read 16 lanes on the 16 chunks of one row: conflict-free both ways.
+      auto put = [&](int c, const float* v) {
+        *reinterpret_cast<f32x4*>(ep + wr * 256 + ((c ^ (wr & 15)) << 4)) = f32x4{v[0], v[1], v[2], v[3]};
+      };
+      const int rc = lane & 15, rr0 = lane >> 4;  // reads: 16 lanes x 4 rows
+      auto stage = [&](int i, int jh, float scale) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int r = (lane >> 4) + 4 * q, c8 = (lane & 15) * 8;
-            float v[8];
-            read8(r, c8, v);
-            epi_chunk<TO, MODE>(P, row0 + r, n0 + wn * 128 + c8, v, v, gq[hh][q], uq[hh][q]);
-            // one chunk at a time: overlapping them costs registers the
-            // aux prefetch needs
-            __builtin_amdgcn_sched_barrier(0);
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = scale * acc_read(acc[i][2 * jh + jj][4 * q + e]);
+            put(8 * jj + 2 * q + wh, v);
           }
+      };
+      auto fetch = [&](int k) {  // row k*4 + rr0 of the staged half, 4 f32
+        const int row = 4 * k + rr0;
+        return *reinterpret_cast<const f32x4*>(ep + row * 256 + ((rc ^ (row & 15)) << 4));
+      };
+      if constexpr (MODE == EPI_STORE) {
+        const float alpha = P.alpha;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const int i = h >> 1, jh = h & 1;
+          stage(i, jh, alpha);
+          wave_lds_sync();
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const f32x4 v = fetch(k);
+            const u32x4 d = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+            __builtin_amdgcn_raw_buffer_store_b128(
+                d, r0, ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldo, ESZ), 0, 0);
+          }
+          wave_lds_sync();
         }
-        wave_lds_sync();
+      } else {
+        static_assert(MODE != EPI_DGDU || ESZ == 2, "the DGDU epilogue reads and writes bf16");
+        // SiLU*up derivative (reference fused_gate_up_bwd_kernel,
+        // src/kernels_elementwise_impl.inc:107-117) on the f32 dInter
+        // values; the saved gate/up pre-activations of a half are loaded
+        // one half ahead.
+        const __amdgpu_buffer_rsrc_t r1 = uni_rsrc(P.out1, kExtent);
+        const __amdgpu_buffer_rsrc_t rG = uni_rsrc(P.aux0, kExtent);
+        const __amdgpu_buffer_rsrc_t rU = uni_rsrc(P.aux1, kExtent);
+        u32x2 ga[2][8], ua[2][8];
+        auto aux = [&](int h) {
+          const int i = h >> 1, jh = h & 1;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const uint32_t o = ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldaux, 2);
+            ga[h & 1][k] = __builtin_amdgcn_raw_buffer_load_b64(rG, o, 0, 0);
+            ua[h & 1][k] = __builtin_amdgcn_raw_buffer_load_b64(rU, o, 0, 0);
+          }
+        };
+        aux(0);
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const int i = h >> 1, jh = h & 1;
+          if (h + 1 < 8) aux(h + 1);
+          stage(i, jh, 1.0f);
+          wave_lds_sync();
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const f32x4 a4 = fetch(k);
+            const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+            const u32x2 gk = ga[h & 1][k], uk = ua[h & 1][k];
+            const float gv[4] = {__uint_as_float(gk.x << 16), __uint_as_float(gk.x & 0xFFFF0000u),
+                                 __uint_as_float(gk.y << 16), __uint_as_float(gk.y & 0xFFFF0000u)};
+            const float uv[4] = {__uint_as_float(uk.x << 16), __uint_as_float(uk.x & 0xFFFF0000u),
+                                 __uint_as_float(uk.y << 16), __uint_as_float(uk.y & 0xFFFF0000u)};
+            float dg[4], du[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float sg = sigmoid_fast(gv[e]);
+              const float sgrad = sg * (1.0f + gv[e] * (1.0f - sg));
+              dg[e] = av[e] * uv[e] * sgrad;
+              du[e] = av[e] * (gv[e] * sg);
+            }
+            const uint32_t o = ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldo, 2);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2_hw(dg[0], dg[1]), pack2_hw(dg[2], dg[3])}, r0, o, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2_hw(du[0], du[1]), pack2_hw(du[2], du[3])}, r1, o, 0, 0);
+          }
+          wave_lds_sync();
+        }
       }
     }
   }
@@ -684,8 +720,12 @@ bool gemm_mfma_eligible(const GemmPlan& plan) {
   }
   for (int p = 0; p < plan.args.nprob; ++p) {
     const GProb& P = plan.args.p[p];
-    // the staged epilogue stores 8-column chunks with 16-byte accesses
-    if (P.ldo % 8 || !al16(P.out0) || !al16(P.out1) || !al16(P.out2)) return false;
+    // the epilogue stores 16-byte column chunks (8 bf16 / 4 f32, so N is a
+    // multiple of that) through 31-bit buffer offsets and never reads the
+    // output (beta = 0)
+    if (P.ldo % 8 || !al16(P.out0) || !al16(P.out1) || !al16(P.out2) || P.beta != 0.f) return false;
+    if (P.N % (P.out_f32 ? 4 : 8) || (int64_t)(P.M + kBM) * P.ldo * (P.out_f32 ? 4 : 2) >= (int64_t)kOob)
+      return false;
     if (P.mode == EPI_DGDU && (P.ldaux % 8 || !al16(P.aux0) || !al16(P.aux1))) return false;
     // the DGDU epilogue reads aux rows through 31-bit buffer offsets
     if (P.mode == EPI_DGDU && (int64_t)(P.M + kBM) * P.ldaux * 2 >= (int64_t)kOob) return false;
