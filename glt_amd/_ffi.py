@@ -17,7 +17,7 @@ STATUS_NAMES = {
     7: "GLT_ERR_BAKED_NO_BACKWARD", 8: "GLT_ERR_HIP", 9: "GLT_ERR_UNSUPPORTED",
 }
 DTYPE_BF16, DTYPE_F32 = 0, 1
-MLP_EXPLICIT, MLP_RECOMPUTE = 1, 2
+MLP_EXPLICIT, MLP_RECOMPUTE, MLP_RESIDUAL = 1, 2, 4
 BAKE_IN_PLACE, BAKE_MATERIALIZE = 0, 1
 GEMM_EXPAND_FWD, GEMM_CONTRACT_FWD, GEMM_EXPAND_WGRAD, GEMM_CONTRACT_WGRAD, GEMM_EXPAND_IGRAD, \
     GEMM_CONTRACT_IGRAD = range(6)

@@ -52,6 +52,10 @@ __device__ __forceinline__ void epilogue(const GProb& P, int m, int n, float a0,
     float v = P.alpha * a0;
     if (P.beta != 0.f) v += P.beta * ld_elem<TO>(P.out0, o);
     st_elem<TO>(P.out0, o, v);
+  } else if constexpr (MODE == EPI_RESID) {
+    // the layer output is rounded to the path dtype, then added to the
+    // residual stream (reference x = x + ffn_out, src/layer_forward_impl.inc:271-275)
+    st_elem<TO>(P.out0, o, ld_elem<TO>(P.out0, o) + round_like<TO>(P.alpha * a0));
   } else if constexpr (MODE == EPI_SILU) {
     // gate/up pre-activations leave the accumulator rounded to the path
     // dtype (bf16 in the reference, src/layer_forward_impl.inc:72,122), and
@@ -474,15 +478,33 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
       constexpr int kLanesPerRow = kPitch / 16, kRowsPerRead = 64 / kLanesPerRow;
       const int rc = lane % kLanesPerRow, rr0 = lane / kLanesPerRow;
       auto drain = [&](__amdgpu_buffer_rsrc_t r, int i) {
+        u32x4 q[32 / kRowsPerRead];
+        uint32_t o[32 / kRowsPerRead];
 #pragma unroll
         for (int k = 0; k < 32 / kRowsPerRead; ++k) {
           const int row = k * kRowsPerRead + rr0;
-          u32x4 q = *reinterpret_cast<const u32x4*>(ep + row * kPitch + ((rc ^ key(row)) << 4));
-          if (k * kRowsPerRead >= 16) q = u32x4{q.z, q.w, q.x, q.y};
-          __builtin_amdgcn_raw_buffer_store_b128(q, r, ooff(rbase + 32 * i + row, cbase + 8 * rc, P.ldo, 2), 0, 0);
+          q[k] = *reinterpret_cast<const u32x4*>(ep + row * kPitch + ((rc ^ key(row)) << 4));
+          if (k * kRowsPerRead >= 16) q[k] = u32x4{q[k].z, q[k].w, q[k].x, q[k].y};
+          o[k] = ooff(rbase + 32 * i + row, cbase + 8 * rc, P.ldo, 2);
         }
+        if constexpr (MODE == EPI_RESID) {
+          // residual rows are read where they are written: 16 bytes per lane
+#pragma unroll
+          for (int k = 0; k < 32 / kRowsPerRead; ++k) {
+            const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o[k], 0, 0));
+            const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+            uint32_t zs[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+              zs[w] = pack2_hw(__uint_as_float(xs[w] << 16) + __uint_as_float(ys[w] << 16),
+                               __uint_as_float(xs[w] & 0xFFFF0000u) + __uint_as_float(ys[w] & 0xFFFF0000u));
+            q[k] = u32x4{zs[0], zs[1], zs[2], zs[3]};
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 32 / kRowsPerRead; ++k) __builtin_amdgcn_raw_buffer_store_b128(q[k], r, o[k], 0, 0);
       };
-      if constexpr (MODE == EPI_STORE) {
+      if constexpr (MODE == EPI_STORE || MODE == EPI_RESID) {
         const float alpha = P.alpha;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -566,7 +588,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
         const int row = 4 * k + rr0;
         return *reinterpret_cast<const f32x4*>(ep + row * 256 + ((rc ^ (row & 15)) << 4));
       };
-      if constexpr (MODE == EPI_STORE) {
+      if constexpr (MODE == EPI_STORE || MODE == EPI_RESID) {
         const float alpha = P.alpha;
 #pragma unroll
         for (int h = 0; h < 8; ++h) {
@@ -575,10 +597,12 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
           wave_lds_sync();
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
-            const f32x4 v = fetch(k);
+            f32x4 v = fetch(k);
+            const uint32_t o = ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldo, ESZ);
+            if constexpr (MODE == EPI_RESID)
+              v += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r0, o, 0, 0));
             const u32x4 d = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
-            __builtin_amdgcn_raw_buffer_store_b128(
-                d, r0, ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldo, ESZ), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(d, r0, o, 0, 0);
           }
           wave_lds_sync();
         }
@@ -805,6 +829,9 @@ glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma) {
     if (mode == EPI_STORE && !plan.dual)
       return of32 ? launch_mfma<float, EPI_STORE, false>(a, st, plan.label)
                   : launch_mfma<uint16_t, EPI_STORE, false>(a, st, plan.label);
+    if (mode == EPI_RESID && !plan.dual)
+      return of32 ? launch_mfma<float, EPI_RESID, false>(a, st, plan.label)
+                  : launch_mfma<uint16_t, EPI_RESID, false>(a, st, plan.label);
     set_error("run_gemm: no MFMA kernel for mode %d dual %d", mode, (int)plan.dual);
     return GLT_ERR_UNSUPPORTED;
   }
@@ -816,10 +843,12 @@ glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma) {
     return launch_generic<LA_, LB_, TO_, MODE_, DUAL_>(a, st, plan.label);
   // f32 path
   GLT_GEN(LD_F32, LD_F32, float, EPI_STORE, false)
+  GLT_GEN(LD_F32, LD_F32, float, EPI_RESID, false)
   GLT_GEN(LD_F32, LD_F32, float, EPI_SILU, true)
   GLT_GEN(LD_F32, LD_F32, float, EPI_DGDU, false)
   // bf16 path on shapes the MFMA kernel does not take
   GLT_GEN(LD_BF16, LD_BF16, uint16_t, EPI_STORE, false)
+  GLT_GEN(LD_BF16, LD_BF16, uint16_t, EPI_RESID, false)
   GLT_GEN(LD_BF16, LD_BF16, float, EPI_STORE, false)
   GLT_GEN(LD_BF16, LD_BF16, uint16_t, EPI_SILU, true)
   GLT_GEN(LD_BF16, LD_BF16, uint16_t, EPI_DGDU, false)

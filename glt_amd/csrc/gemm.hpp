@@ -23,6 +23,7 @@ enum EpiMode : int {
   EPI_STORE = 0,  // out0 = alpha*acc + beta*out0
   EPI_SILU = 1,   // dual: out0 = silu(g)*u, out1 = g, out2 = u (out1/out2 nullable)
   EPI_DGDU = 2,   // out0 = acc*u*silu'(g), out1 = acc*silu(g); g = aux0, u = aux1
+  EPI_RESID = 3,  // out0 = round(out0 + round(alpha*acc)): residual add of a rounded result
 };
 
 // Element kinds an operand can be read as. LD_SHUF: bf16 B operand in the

@@ -132,7 +132,8 @@ static glt_status down_forward(const glt_mlp_desc* d, const glt_base_weights* w,
   GemmPlan plan;
   plan.label = "down";
   set_kinds(plan, d, mfma);
-  plan.add_problem(prob(d->M, d->D, EPI_STORE, f32, y, nullptr, nullptr, d->D));
+  plan.add_problem(prob(d->M, d->D, (d->flags & GLT_MLP_RESIDUAL) ? EPI_RESID : EPI_STORE, f32, y, nullptr, nullptr,
+                        d->D));
   if (d->I > 0) plan.add_seg(nt_seg(inter, d->N, 0, d->I, 0, d->D, mfma ? prep(d, w, PREP_DOWN) : w->down, d->I, 0));
   if (d->flags & GLT_MLP_EXPLICIT) {
     for (int j = 0; j < d->n_slices; ++j) {

@@ -99,20 +99,24 @@ class BaseMLP:
         return F.BaseWeights(_p(self.gate), _p(self.up), _p(self.down), _p(self.prepared))
 
 
-def _desc(base, slices, M, N, explicit, recompute=False, state=None):
+def _desc(base, slices, M, N, explicit, recompute=False, state=None, residual=False):
     arr = _slices_array(slices)
-    flags = (F.MLP_EXPLICIT if explicit else 0) | (F.MLP_RECOMPUTE if recompute else 0)
+    flags = ((F.MLP_EXPLICIT if explicit else 0) | (F.MLP_RECOMPUTE if recompute else 0)
+             | (F.MLP_RESIDUAL if residual else 0))
     d = F.MlpDesc(M, base.D, base.I, N, _dtype_code(base.dtype), flags, len(slices), arr,
                   ctypes.pointer(state) if state is not None else None)
     return d, arr
 
 
-def mlp_forward(base, slices, x, N, explicit=True, save=True):
+def mlp_forward(base, slices, x, N, explicit=True, save=True, residual=None):
     """Grafted SwiGLU forward (reference forward_layer FFN section,
-    src/layer_forward_impl.inc:61-290). Returns y, gate_pre, up_pre, inter."""
+    src/layer_forward_impl.inc:61-290). Returns y, gate_pre, up_pre, inter.
+    With `residual` ([M,D], updated in place and returned as y) the output is
+    added to it in the down GEMM's epilogue (reference x = x + ffn_out,
+    src/layer_forward_impl.inc:271-275)."""
     M = x.shape[0]
-    d, keep = _desc(base, slices, M, N, explicit)
-    y = torch.empty((M, base.D), dtype=base.dtype, device=x.device)
+    d, keep = _desc(base, slices, M, N, explicit, residual=residual is not None)
+    y = residual if residual is not None else torch.empty((M, base.D), dtype=base.dtype, device=x.device)
     inter = torch.empty((M, N), dtype=base.dtype, device=x.device)
     g = torch.empty_like(inter) if save else None
     u = torch.empty_like(inter) if save else None

@@ -117,6 +117,11 @@ typedef struct {
  * its workspace instead of reading saved activations (the reference's
  * recompute_ffn, src/layer_recompute_impl.inc:8-91). */
 #define GLT_MLP_RECOMPUTE 2
+/* GLT_MLP_RESIDUAL: y holds the residual stream on entry and glt_mlp_fwd
+ * adds the MLP output to it in the down GEMM's epilogue,
+ * y = round(y + round(ffn_out)) (the reference's x = x + ffn_out,
+ * src/layer_forward_impl.inc:271-275, on the path dtype). */
+#define GLT_MLP_RESIDUAL 4
 typedef struct {
   int32_t M, D, I, N;
   int32_t dtype;   /* GLT_DTYPE_BF16 or GLT_DTYPE_F32 */

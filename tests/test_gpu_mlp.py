@@ -159,3 +159,33 @@ def test_test6_f32_explicit_equals_baked(dev):
         md = np.max(np.abs(a - b))
         mv = np.max(np.maximum(np.abs(a), np.abs(b)))
         assert md < 1e-4 or md / mv < 1e-6, (nm, md, mv)
+
+
+@pytest.mark.parametrize("M,D,I,S,bf16", [(512, 512, 1024, 256, True),    # MFMA path
+                                          (100, 200, 300, 40, True),      # generic bf16 path
+                                          (64, 128, 192, 64, False)])     # f32 path
+def test_residual_fused_in_down_epilogue(dev, M, D, I, S, bf16):
+    """GLT_MLP_RESIDUAL: y = round(residual + round(ffn_out)) written by the
+    down GEMM's epilogue, bit-for-bit the reference's x = x + ffn_out on the
+    path dtype (src/layer_forward_impl.inc:271-275) over the plain output."""
+    import torch
+    from glt_amd import ops, synth
+    dt = torch.bfloat16 if bf16 else torch.float32
+    N = I + S
+    wg, wu, wd, sl = make_layer(D, I, N, [(I, S, 0, D)], bf16)
+    base = ops.BaseMLP(to_dev(wg, dt), to_dev(wu, dt), to_dev(wd, dt))
+    gs = [ops.GraftSlice(s["i0"], s["s"], s["h0"], s["h"],
+                         *(to_dev(s[p], torch.float32) for p in ("gate", "up", "down"))).pack() for s in sl]
+    x = to_dev(draw((M, D), 100, synth.TID_X, 0, 1, bf16), dt)
+    res = draw((M, D), 7, 77, 0, 1, bf16)
+    y, _, _, _ = ops.mlp_forward(base, gs, x, N)
+    yr_in = to_dev(res, dt)
+    yr, _, _, _ = ops.mlp_forward(base, gs, x, N, residual=yr_in)
+    torch.cuda.synchronize()
+    assert yr.data_ptr() == yr_in.data_ptr()
+    ffn = to_np(y)
+    if bf16:
+        exp = O.f32_to_bf16_bits(res.astype(np.float32) + ffn)
+        np.testing.assert_array_equal(yr.view(torch.int16).cpu().numpy().view(np.uint16), exp)
+    else:
+        np.testing.assert_array_equal(to_np(yr), res + ffn)
