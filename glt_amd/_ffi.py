@@ -83,6 +83,7 @@ SIGNATURES = {
     "glt_rmsnorm_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "glt_rmsnorm_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "glt_rope_fwd": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
+    "glt_attention_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
     "glt_adamw_workspace_size": (_sz, [_i64]),
     "glt_adamw_step": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _f32, _f32, _f32, _f32, _f32, _f32, _vp, _sz,
                               _vp]),

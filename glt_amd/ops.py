@@ -186,6 +186,20 @@ def apply_rope(q, k, theta, pos_offset=0):
     F.call("glt_rope_fwd", _p(q), nq, _p(k), nk, B, T, hd, theta, pos_offset, _stream())
 
 
+def attention(q, k, v, causal=True, scale=None):
+    """Causal GQA attention forward (the reference's SDPA call in
+    forward_layer, src/layer_forward_impl.inc:41-49). q [B,T,Hq,hd],
+    k/v [B,T,Hkv,hd] bf16; returns [B,T,Hq,hd]."""
+    B, T, Hq, hd = q.shape
+    Hkv = k.shape[2]
+    if scale is None:
+        scale = hd ** -0.5
+    out = torch.empty_like(q)
+    F.call("glt_attention_fwd", _p(q), _p(k), _p(v), _p(out), B, T, Hq, Hkv, hd, scale, 1 if causal else 0,
+           _stream())
+    return out
+
+
 def adamw_step(w, g, m, v, step, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, clip_norm=0.0,
                mirror=None):
     """One AdamW step (reference adamw_fused_kernel + optional global clip)."""

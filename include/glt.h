@@ -268,6 +268,21 @@ glt_status glt_rope_fwd(uint16_t* q, int32_t n_q_heads, uint16_t* k, int32_t n_k
                         int32_t B, int32_t T, int32_t head_dim, float theta,
                         int32_t pos_offset, void* stream);
 
+/* -------------------------------------------------------------- Attention */
+/* Causal GQA attention forward, the decoder layer's base attention
+ * (reference forward_layer src/layer_forward_impl.inc:41-49: heads split,
+ * k/v repeat_interleave'd to the query heads, at::scaled_dot_product_attention
+ * with is_causal, heads merged). q/out [B,T,n_q_heads,head_dim], k/v
+ * [B,T,n_kv_heads,head_dim], bf16 row-major; query head h reads kv head
+ * h / (n_q_heads / n_kv_heads). scale multiplies q.k (the reference's default
+ * is 1/sqrt(head_dim)); causal != 0 masks keys after the query's position.
+ * Softmax in f32 (online, exp2), probabilities rounded to bf16 for the P.V
+ * product, f32 accumulation, one rounding of the output. head_dim must be
+ * 128; tensors 16-byte aligned. */
+glt_status glt_attention_fwd(const void* q, const void* k, const void* v, void* out,
+                             int32_t B, int32_t T, int32_t n_q_heads, int32_t n_kv_heads,
+                             int32_t head_dim, float scale, int32_t causal, void* stream);
+
 /* ------------------------------------------------------------------ AdamW */
 /* One AdamW step over n f32 params (reference adamw_fused_kernel,
  * src/kernels_optimizer_impl.inc:11-77) with bias corrections for step

@@ -164,6 +164,32 @@ def rope(t, theta, pos_offset=0, exact_rounding=True):
     return t
 
 
+# ------------------------------------------------------------- attention
+def attention(q, k, v, causal=True, scale=None):
+    """Scaled-dot-product attention in float64, the reference's base
+    attention (forward_layer, src/layer_forward_impl.inc:41-49): query head h
+    reads kv head h // (Hq // Hkv) (k/v repeat_interleave'd over heads,
+    :46-47), softmax(scale * q.k^T) with keys after the query masked when
+    causal (SDPA is_causal, :48), then . v. q [B,T,Hq,hd], k/v [B,T,Hkv,hd];
+    returns [B,T,Hq,hd] float64."""
+    B, T, Hq, hd = q.shape
+    Hkv = k.shape[2]
+    rep = Hq // Hkv
+    scale = hd ** -0.5 if scale is None else scale
+    out = np.zeros((B, T, Hq, hd))
+    future = np.triu(np.ones((T, T), bool), 1) if causal else np.zeros((T, T), bool)
+    for b in range(B):
+        for h in range(Hq):
+            g = h // rep
+            s = (np.asarray(q[b, :, h], np.float64) @ np.asarray(k[b, :, g], np.float64).T) * scale
+            s[future] = -np.inf
+            s -= s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(axis=1, keepdims=True)
+            out[b, :, h] = p @ np.asarray(v[b, :, g], np.float64)
+    return out
+
+
 # ---------------------------------------------------------------- AdamW
 def adamw(w, g, m, v, step, lr, b1, b2, eps, wd, clip_norm=0.0):
     w, g, m, v = _c32(w).copy(), _c32(g), _c32(m).copy(), _c32(v).copy()

@@ -46,6 +46,8 @@ def test_host_validation_errors_without_gpu():
     assert rc == 7  # GLT_ERR_BAKED_NO_BACKWARD (reference src/layer_backward_impl.inc:11-13)
     bd = F.BakeDesc(0, 1, 0, 0, 7, 64, 64, 64, F.DTYPE_F32, 0, None, None)
     assert lib.glt_shadow_bake(ctypes.byref(bd), ctypes.byref(st), None, None, None, None, None, None, None) == 6
+    # attention supports head_dim 128 only; refused before any GPU call
+    assert lib.glt_attention_fwd(1, 1, 1, 1, 1, 16, 4, 1, 64, 0.125, 1, None) == 9  # GLT_ERR_UNSUPPORTED
     d2 = F.MlpDesc(16, 64, 128, 64, F.DTYPE_BF16, 0, 0, None, None)  # N < I
     assert lib.glt_mlp_fwd(ctypes.byref(d2), ctypes.byref(w), 1, 1, None, None, 1, None) == 2
     d3 = F.MlpDesc(16, 64, 64, 64, 7, 0, 0, None, None)

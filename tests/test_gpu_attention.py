@@ -1,0 +1,49 @@
+"""GPU parity of the causal GQA attention forward (glt_attention_fwd)
+against the float64 oracle (the reference's SDPA call in forward_layer,
+src/layer_forward_impl.inc:41-49)."""
+import numpy as np
+import pytest
+
+from helpers import assert_bf16_budget, draw, to_dev, to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,causal", [
+    (1, 128, 4, 1, True),     # one query block, 4 query heads per kv head
+    (2, 200, 8, 2, True),     # ragged last query block and key tile
+    (1, 64, 2, 2, True),      # no head grouping
+    (1, 300, 4, 2, False),    # non-causal
+    (1, 1, 4, 1, True),       # a single token
+    (1, 520, 32, 8, True),    # the decoder layer's head layout, several key tiles per block
+])
+def test_attention_vs_oracle(dev, B, T, Hq, Hkv, causal):
+    """bf16 budget with q = 3 roundings: probabilities, output, inputs."""
+    import torch
+    from glt_amd import ops
+    hd = 128
+    q = draw((B, T, Hq, hd), 11, 1)
+    k = draw((B, T, Hkv, hd), 11, 2)
+    v = draw((B, T, Hkv, hd), 11, 3)
+    bf = torch.bfloat16
+    out = ops.attention(to_dev(q, bf), to_dev(k, bf), to_dev(v, bf), causal=causal)
+    torch.cuda.synchronize()
+    ref = O.attention(q, k, v, causal=causal)
+    assert_bf16_budget(to_np(out), ref, q=3, what=f"attention B={B} T={T} Hq={Hq} Hkv={Hkv} causal={causal}")
+
+
+def test_attention_uniform_queries_give_prefix_means(dev):
+    """q = 0 makes every allowed key equally likely: row t of the output is
+    the mean of v[0..t] of its kv head (mask direction and head map)."""
+    import torch
+    from glt_amd import ops
+    B, T, Hq, Hkv, hd = 1, 150, 8, 2, 128
+    v = draw((B, T, Hkv, hd), 12, 3)
+    k = draw((B, T, Hkv, hd), 12, 2)
+    bf = torch.bfloat16
+    out = to_np(ops.attention(torch.zeros((B, T, Hq, hd), dtype=bf, device="cuda"), to_dev(k, bf), to_dev(v, bf)))
+    for h in range(Hq):
+        g = h // (Hq // Hkv)
+        prefix = np.cumsum(v[0, :, g].astype(np.float64), axis=0) / np.arange(1, T + 1)[:, None]
+        assert_bf16_budget(out[0, :, h], prefix, q=3, what=f"head {h}")

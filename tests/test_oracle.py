@@ -178,6 +178,54 @@ def test_rope_matches_aten_sequence_and_invariants():
     np.testing.assert_array_equal(a, got[:, 5:])
 
 
+# ------------------------------------------------------------ attention
+def test_attention_closed_forms():
+    """Pins what a plausible mistake would change: the causal mask direction
+    (key <= query), the GQA head map (repeat_interleave: query head h uses kv
+    head h // rep, not h % Hkv), the scale, and T = 1."""
+    B, T, Hq, Hkv, hd = 2, 7, 4, 2, 8
+    rng = np.random.default_rng(3)
+    v = rng.normal(size=(B, T, Hkv, hd))
+    k = rng.normal(size=(B, T, Hkv, hd))
+    # q = 0: uniform weights over the allowed keys -> causal prefix mean of v
+    out = O.attention(np.zeros((B, T, Hq, hd)), k, v, causal=True)
+    for h in range(Hq):
+        g = h // (Hq // Hkv)
+        prefix = np.cumsum(v[:, :, g], axis=1) / np.arange(1, T + 1)[None, :, None]
+        np.testing.assert_allclose(out[:, :, h], prefix, rtol=1e-12, atol=1e-12)
+    # non-causal: the full mean for every query
+    full = O.attention(np.zeros((B, T, Hq, hd)), k, v, causal=False)
+    np.testing.assert_allclose(full[:, :, 1], np.broadcast_to(v[:, :, 0].mean(axis=1, keepdims=True), (B, T, hd)),
+                               rtol=1e-12, atol=1e-12)
+    # a query aligned with one earlier key at a large scale picks that key's value
+    kk = np.zeros((1, 4, 1, 4))
+    kk[0, :, 0, :] = np.eye(4)
+    vv = np.arange(16, dtype=np.float64).reshape(1, 4, 1, 4)
+    qq = np.zeros((1, 4, 1, 4))
+    qq[0, 3, 0, 1] = 1.0  # query 3 matches key 1
+    sharp = O.attention(qq, kk, vv, causal=True, scale=200.0)
+    np.testing.assert_allclose(sharp[0, 3, 0], vv[0, 1, 0], atol=1e-9)
+    # T = 1: the output is v whatever q is
+    one = O.attention(rng.normal(size=(1, 1, 2, 8)), rng.normal(size=(1, 1, 1, 8)), v[:1, :1, :1], causal=True)
+    np.testing.assert_allclose(one[0, 0, 1], v[0, 0, 0], rtol=1e-12)
+
+
+def test_attention_matches_torch_sdpa():
+    """torch's CPU scaled_dot_product_attention (a library routine, float64)
+    on repeat_interleave'd k/v, as the reference calls it."""
+    import torch
+    B, T, Hq, Hkv, hd = 2, 19, 6, 2, 16
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.normal(size=(B, T, H, hd)) for H in (Hq, Hkv, Hkv))
+    for causal in (True, False):
+        got = O.attention(q, k, v, causal=causal)
+        tq, tk, tv = (torch.from_numpy(a).transpose(1, 2) for a in (q, k, v))
+        tk = tk.repeat_interleave(Hq // Hkv, 1)
+        tv = tv.repeat_interleave(Hq // Hkv, 1)
+        ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=causal).transpose(1, 2).numpy()
+        np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
 # ----------------------------------------------------------------- AdamW
 def test_adamw_closed_form_step0_and_torch():
     rng = np.random.default_rng(5)
