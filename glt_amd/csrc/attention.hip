@@ -37,6 +37,7 @@ constexpr int kKBytes = kKvTile * kHd * 2;   // 16 KB
 constexpr int kStageBytes = 2 * kKBytes;     // K + V^T
 constexpr int kAttnLds = 2 * kStageBytes;    // 64 KB
 constexpr float kMaskVal = -1.0e30f;         // finite: no inf - inf
+constexpr float kSlack = 8.0f;               // running-max slack (log2 units)
 constexpr uint32_t kExtentA = 0x7FFFFFF0u;   // buffer extent below kOob
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -129,6 +130,13 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
                       : u32x4{0, 0, 0, 0};
     }
   };
+  // V^T write offsets of this thread's eight rows (the same every tile)
+  uint32_t vto[8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    vto[2 * p] = vt_off(8 * vdc + 2 * p, vkg >> 1, vkg & 1);
+    vto[2 * p + 1] = vt_off(8 * vdc + 2 * p + 1, vkg >> 1, vkg & 1);
+  }
   auto store_vt = [&](int stage) {
     char* dst = smem + stage * kStageBytes + kKBytes;
     const uint32_t w0[4] = {vr[0].x, vr[1].x, vr[2].x, vr[3].x};
@@ -142,9 +150,8 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
       const uint32_t* x = wd[p];
       const uint32_t lo01 = (x[0] & 0xFFFFu) | (x[1] << 16), lo23 = (x[2] & 0xFFFFu) | (x[3] << 16);
       const uint32_t hi01 = (x[0] >> 16) | (x[1] & 0xFFFF0000u), hi23 = (x[2] >> 16) | (x[3] & 0xFFFF0000u);
-      const int R = 8 * vdc + 2 * p;
-      *reinterpret_cast<u32x2a*>(dst + vt_off(R, vkg >> 1, vkg & 1)) = u32x2a{lo01, lo23};
-      *reinterpret_cast<u32x2a*>(dst + vt_off(R + 1, vkg >> 1, vkg & 1)) = u32x2a{hi01, hi23};
+      *reinterpret_cast<u32x2a*>(dst + vto[2 * p]) = u32x2a{lo01, lo23};
+      *reinterpret_cast<u32x2a*>(dst + vto[2 * p + 1]) = u32x2a{hi01, hi23};
     }
   };
 
@@ -186,23 +193,36 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
           sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[kb], 0, 0, 0);
         }
       }
-      // scale, mask, tile maximum over the query's 64 keys (lane pair)
+      // Mask (only a tile that reaches past this wavefront's first query
+      // or past T needs it): key index < lim, with lim the lane's causal /
+      // sequence bound relative to this lane's first key of the tile.
       const int key0 = t * kKvTile;
+      if (key0 + kKvTile > T || (causal && key0 + kKvTile - 1 > wq0)) {
+        const int lim = (causal ? min(T, myq + 1) : T) - (key0 + 4 * lh);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            sacc[kb][e] = (32 * kb + 8 * (e >> 2) + (e & 3)) < lim ? sacc[kb][e] : kMaskVal;
+      }
+      // tile maximum of the query's 64 scores (lane pair), in exp2 units
       float mt = kMaskVal;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = key0 + 32 * kb + 8 * (e >> 2) + 4 * lh + (e & 3);
-          float sv = sacc[kb][e] * scale_log2;
-          if (key >= T || (causal && key > myq)) sv = kMaskVal;
-          sacc[kb][e] = sv;
-          mt = fmaxf(mt, sv);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
+        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sacc[kb][e]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * scale_log2;
+      // The running maximum moves only when some lane's grows by more than
+      // kSlack: probabilities then stay below 2^kSlack, the same result up
+      // to rounding, and O is rescaled on few tiles.
+      if (__any(mt > m_run + kSlack)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] *= alpha;
+      }
       float psum = 0.f;
       uint32_t pk[2][4][2];  // [kb][group][packed pair]: 4 probabilities of the group
 #pragma unroll
@@ -212,16 +232,13 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
           float p4[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float sv = sacc[kb][4 * gi + e];
-            p4[e] = sv <= kMaskVal ? 0.f : __builtin_amdgcn_exp2f(sv - m_new);
+            p4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][4 * gi + e], scale_log2, -m_run));
             psum += p4[e];
           }
           pk[kb][gi][0] = pack2_rne(p4[0], p4[1]);
           pk[kb][gi][1] = pack2_rne(p4[2], p4[3]);
         }
-      l_run = l_run * alpha + psum;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] *= alpha;
+      l_run += psum;
       // O^T += V^T . P^T over four 16-key steps: step s2 covers keys
       // 16 s2 .. +15 = groups 2(s2&1), 2(s2&1)+1 of block s2>>1. The lane
       // with lh = 0 needs keys +0..7 (its own first four, its partner's
