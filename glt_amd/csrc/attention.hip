@@ -64,14 +64,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uni_rsrc_a(const void* p, uint
 
 __global__ void __launch_bounds__(256, 2)
 attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                uint16_t* __restrict__ out, int T, int Hq, int Hkv, float scale_log2, int causal) {
+                uint16_t* __restrict__ out, int B, int T, int Hq, int Hkv, float scale_log2, int causal) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Block order: query blocks longest-first; within a rank, (batch, head)
+  // with the kv head fastest. Workgroups are dealt round-robin over the 8
+  // XCDs, so one XCD's workgroups share kv heads (and their K/V in its L2).
   const int nqb = (T + kQBlock - 1) / kQBlock;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int g = h / (Hq / Hkv);
+  const int rep = Hq / Hkv, nhb = Hq * B;
+  const int id = blockIdx.x;
+  const int qb = nqb - 1 - id / nhb;
+  const int hb = id % nhb;
+  const int g = hb % Hkv, h = g * rep + (hb / Hkv) % rep, b = hb / Hq;
   const int q0 = qb * kQBlock;
   const int wq0 = q0 + 32 * wave;                    // this wavefront's first query
   const int lq = lane & 31, lh = lane >> 5;
@@ -181,18 +186,25 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
       const char* kt = smem + st * kStageBytes;
       const char* vt = kt + kKBytes;
       // S^T blocks: keys 32kb + (8(e>>2) + 4lh + (e&3)), query lq
-      f32x16 sacc[2];
+      // four independent accumulation chains (two key blocks x two halves
+      // of d), merged after: a dependent MFMA waits for its predecessor
+      f32x16 sacc[2], spart[2][2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        sacc[kb] = f32x16{};
-        const int r = 32 * kb + lq;
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int c = 2 * s + lh;
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + r * 256 + ((c ^ (r & 15)) << 4));
-          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[kb], 0, 0, 0);
-        }
-      }
+        for (int hf = 0; hf < 2; ++hf) spart[kb][hf] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            const int r = 32 * kb + lq, c = 2 * (4 * hf + s) + lh;
+            const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + r * 256 + ((c ^ (r & 15)) << 4));
+            spart[kb][hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[4 * hf + s], spart[kb][hf], 0, 0, 0);
+          }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) sacc[kb] = spart[kb][0] + spart[kb][1];
       // Mask (only a tile that reaches past this wavefront's first query
       // or past T needs it): key index < lim, with lim the lane's causal /
       // sequence bound relative to this lane's first key of the tile.
@@ -260,7 +272,8 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
         }
       }
     }
-    __syncthreads();  // stage st is refilled two tiles later
+    // no second barrier: stage st is next written after the first barrier
+    // of tile t+1, which every wavefront reaches only once done with tile t
   }
 
   // ---- normalise and store: lane holds d = 32hb + 8(e>>2) + 4lh + (e&3)
@@ -298,17 +311,19 @@ extern "C" glt_status glt_attention_fwd(const void* q, const void* k, const void
   // K rows are addressed through 31-bit buffer offsets
   GLT_CHECK((int64_t)B * T * Hkv * kHd * 2 < (int64_t)kOob, GLT_ERR_SHAPE, "glt_attention_fwd: K of %lld bytes",
             (long long)B * T * Hkv * kHd * 2);
-  GLT_CHECK(B <= 65535 && Hq <= 65535, GLT_ERR_SHAPE, "glt_attention_fwd: grid B=%d Hq=%d", B, Hq);
   static bool attr_set = false;
   if (!attr_set) {
     GLT_TRY_HIP(hipFuncSetAttribute((const void*)attn_fwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kAttnLds));
     attr_set = true;
   }
   const float scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid((unsigned)((T + kQBlock - 1) / kQBlock), (unsigned)Hq, (unsigned)B);
+  // 1-D over (query block, batch, head)
+  const int64_t nblk = (int64_t)((T + kQBlock - 1) / kQBlock) * Hq * B;
+  GLT_CHECK(nblk < INT32_MAX, GLT_ERR_SHAPE, "glt_attention_fwd: %lld workgroups", (long long)nblk);
+  dim3 grid((unsigned)nblk, 1, 1);
   GLT_LAUNCH("attention", attn_fwd_kernel, grid, dim3(256), kAttnLds, as_stream(stream),
              static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-             static_cast<uint16_t*>(out), T, Hq, Hkv, scale_log2, causal);
+             static_cast<uint16_t*>(out), B, T, Hq, Hkv, scale_log2, causal);
   GLT_LAUNCH_CHECK("attention");
   return GLT_OK;
 }
