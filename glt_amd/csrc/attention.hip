@@ -16,7 +16,7 @@
 // so the online-softmax statistics of a query live in the lane pair
 // (l, l^32) and the rescale of O is one multiply per accumulator. The P^T
 // operand of a 16-key step takes four of the lane's probabilities and four
-// of its partner's (one lane exchange).
+// of its partner's (one v_permlane32_swap per register).
 //
 // LDS per stage: the K tile as [64 keys][128 d] (direct-to-LDS loads, 16-byte
 // chunk c of row r at c ^ (r & 15)) and the V^T tile as [128 d][64 keys]
@@ -48,6 +48,19 @@ __device__ __forceinline__ uint32_t pack2_rne(float a, float b) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const bf16x2_t v = {(__bf16)a, (__bf16)b};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// v_permlane32_swap(a, b) returns r0 = [a of lanes 0-31 | b of lanes 0-31]
+// and r1 = [a of lanes 32-63 | b of lanes 32-63] (lanes 0-31 | 32-63).
+// For a value held per lane, r0/r1 of swap(x, x) are the values of the two
+// lanes of the pair (l, l^32), in every lane.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ uint32_t vt_off(int R, int c, int half) {
@@ -223,7 +236,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sacc[kb][e]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * scale_log2;
+      mt = pair_max(mt) * scale_log2;
       // The running maximum moves only when some lane's grows by more than
       // kSlack: probabilities then stay below 2^kSlack, the same result up
       // to rounding, and O is rescaled on few tiles.
@@ -254,17 +267,15 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
       // O^T += V^T . P^T over four 16-key steps: step s2 covers keys
       // 16 s2 .. +15 = groups 2(s2&1), 2(s2&1)+1 of block s2>>1. The lane
       // with lh = 0 needs keys +0..7 (its own first four, its partner's
-      // next four), lh = 1 keys +8..15.
+      // next four), lh = 1 keys +8..15: swap(own g0, own g1) gives lanes
+      // 0-31 their g0 keys +0..3 (r0) and the partner's +4..7 (r1), lanes
+      // 32-63 the partner's g1 keys +0..3 (r0) and their own +4..7 (r1).
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
         const int kb = s2 >> 1, g0 = 2 * (s2 & 1), g1 = g0 + 1;
-        uint32_t x0 = pk[kb][g0][0], x1 = pk[kb][g0][1], y0 = pk[kb][g1][0], y1 = pk[kb][g1][1];
-        const uint32_t s0 = lh ? x0 : y0, s1 = lh ? x1 : y1;
-        const uint32_t r0 = __shfl_xor((int)s0, 32, 64), r1 = __shfl_xor((int)s1, 32, 64);
-        u32x4 pf;
-        if (lh == 0) pf = u32x4{x0, x1, r0, r1};
-        else pf = u32x4{r0, r1, y0, y1};
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, pf);
+        const auto s0 = __builtin_amdgcn_permlane32_swap(pk[kb][g0][0], pk[kb][g1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(pk[kb][g0][1], pk[kb][g1][1], false, false);
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{s0[0], s1[0], s0[1], s1[1]});
 #pragma unroll
         for (int hb = 0; hb < 4; ++hb) {
           const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vt + vt_off(32 * hb + lq, 2 * s2 + lh, 0));
@@ -277,7 +288,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
   }
 
   // ---- normalise and store: lane holds d = 32hb + 8(e>>2) + 4lh + (e&3)
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if (myq < T) {
     uint16_t* op = out + ((int64_t)b * T + myq) * q_ld + (int64_t)h * kHd + 4 * lh;
