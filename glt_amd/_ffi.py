@@ -57,6 +57,16 @@ class BakeDesc(ctypes.Structure):
                 ("n_slices", _i32), ("placement", ctypes.POINTER(_i32)), ("graft", ctypes.POINTER(_vp))]
 
 
+class LayerDesc(ctypes.Structure):
+    _fields_ = [("B", _i32), ("T", _i32), ("n_q_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
+                ("rope_theta", _f32), ("rms_eps", _f32), ("mlp", MlpDesc)]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [("q_proj", _vp), ("k_proj", _vp), ("v_proj", _vp), ("o_proj", _vp), ("ln_in", _vp),
+                ("ln_post", _vp), ("prepared", _vp), ("mlp", BaseWeights)]
+
+
 # name -> (restype, argtypes): every entry point declared in include/glt.h
 SIGNATURES = {
     "glt_version": (_i32, []),
@@ -84,6 +94,11 @@ SIGNATURES = {
     "glt_rmsnorm_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "glt_rope_fwd": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
     "glt_attention_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
+    "glt_attn_prepared_size": (_sz, [ctypes.POINTER(LayerDesc)]),
+    "glt_attn_prepare": (_i32, [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerWeights), _vp, _vp]),
+    "glt_layer_fwd_workspace_size": (_sz, [ctypes.POINTER(LayerDesc)]),
+    "glt_layer_fwd": (_i32, [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerWeights), _vp, _vp, _vp, _vp, _vp, _vp,
+                             _vp, _sz, _vp]),
     "glt_adamw_workspace_size": (_sz, [_i64]),
     "glt_adamw_step": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _f32, _f32, _f32, _f32, _f32, _f32, _vp, _sz,
                               _vp]),

@@ -267,3 +267,32 @@ def gate_up_bwd(gi, g, u):
     du = torch.empty_like(dg)
     F.call("glt_gate_up_bwd", _p(gi), _p(g), _p(u), _p(dg), _p(du), gi.numel(), _stream())
     return dg, du
+
+
+class DecoderLayer:
+    """One decoder layer with the grafted MLP (reference forward_layer,
+    src/layer_forward_impl.inc:15-290) over glt_layer_fwd. Projection weights
+    bf16 [out, in]; base is the MLP's BaseMLP; slices its graft slices."""
+
+    def __init__(self, B, T, n_q_heads, n_kv_heads, wq, wk, wv, wo, ln_in, ln_post, base, slices, N,
+                 rope_theta=500000.0, rms_eps=1e-5, explicit=True, head_dim=128):
+        self.base, self.slices = base, slices
+        md, self._keep = _desc(base, slices, B * T, N, explicit)
+        self.desc = F.LayerDesc(B, T, n_q_heads, n_kv_heads, head_dim, rope_theta, rms_eps, md)
+        self._w = (wq, wk, wv, wo, ln_in, ln_post)
+        self.prepared = torch.empty(F.load().glt_attn_prepared_size(ctypes.byref(self.desc)), dtype=torch.uint8,
+                                    device=wq.device)
+        self.weights = F.LayerWeights(_p(wq), _p(wk), _p(wv), _p(wo), _p(ln_in), _p(ln_post), _p(self.prepared),
+                                      base.c_struct())
+        F.call("glt_attn_prepare", ctypes.byref(self.desc), ctypes.byref(self.weights), _p(self.prepared), _stream())
+        self.ws = torch.empty(F.load().glt_layer_fwd_workspace_size(ctypes.byref(self.desc)), dtype=torch.uint8,
+                              device=wq.device)
+
+    def forward(self, x, inter=None):
+        """x [B*T, D] bf16, updated in place; returns (x, x_ffn, ffn_var)."""
+        M, D = x.shape
+        x_ffn = torch.empty_like(x)
+        var = torch.empty(M, dtype=torch.float32, device=x.device)
+        F.call("glt_layer_fwd", ctypes.byref(self.desc), ctypes.byref(self.weights), _p(x), _p(x_ffn), _p(var),
+               None, None, _p(inter), _p(self.ws), self.ws.numel(), _stream())
+        return x, x_ffn, var

@@ -283,6 +283,51 @@ glt_status glt_attention_fwd(const void* q, const void* k, const void* v, void* 
                              int32_t B, int32_t T, int32_t n_q_heads, int32_t n_kv_heads,
                              int32_t head_dim, float scale, int32_t causal, void* stream);
 
+/* ---------------------------------------------------------- decoder layer */
+/* One decoder layer forward with the grafted MLP (reference forward_layer,
+ * src/layer_forward_impl.inc:15-290):
+ *   xn = rms_norm(x, ln_in); q,k,v = xn . W^T; RoPE(q, k); a = SDPA(q,k,v)
+ *   x += a . W_o^T; x_ffn = rms_norm(x, ln_post); x += grafted_mlp(x_ffn)
+ * bf16 throughout; M = B*T tokens, x [M,D] is the residual stream, updated
+ * in place. rope_theta <= 0 skips RoPE (the reference's no-RoPE layer mask,
+ * :37-39). mlp is the MLP's descriptor (mlp.M = B*T, mlp.D = D, bf16). */
+typedef struct {
+  int32_t B, T;
+  int32_t n_q_heads, n_kv_heads, head_dim; /* head_dim 128 */
+  float rope_theta;
+  float rms_eps;
+  glt_mlp_desc mlp;
+} glt_layer_desc;
+
+/* Projection weights are bf16 [out, in] row-major like torch Linear (the
+ * reference's q_proj/k_proj/v_proj/o_proj, src/types.hpp); ln_* are the two
+ * RMSNorm weights [D]; prepared holds them in the MFMA fragment layout
+ * (glt_attn_prepare); mlp is the MLP's base. */
+typedef struct {
+  const void* q_proj;
+  const void* k_proj;
+  const void* v_proj;
+  const void* o_proj;
+  const void* ln_in;
+  const void* ln_post;
+  const void* prepared;
+  glt_base_weights mlp;
+} glt_layer_weights;
+
+size_t glt_attn_prepared_size(const glt_layer_desc* d);
+/* Writes the four projections of w into prepared (glt_attn_prepared_size
+ * bytes, 256-byte aligned); once per frozen layer. */
+glt_status glt_attn_prepare(const glt_layer_desc* d, const glt_layer_weights* w, void* prepared,
+                            void* stream);
+size_t glt_layer_fwd_workspace_size(const glt_layer_desc* d);
+/* x_ffn [M,D] bf16 and ffn_var [M] f32 (the MLP input and its RMSNorm
+ * mean square) are written for the backward; gate_pre/up_pre/inter are the
+ * MLP's saved activations as in glt_mlp_fwd (nullable: then they live in the
+ * workspace and glt_mlp_bwd recomputes, the reference's recompute_ffn). */
+glt_status glt_layer_fwd(const glt_layer_desc* d, const glt_layer_weights* w, void* x, void* x_ffn,
+                         float* ffn_var, void* gate_pre, void* up_pre, void* inter, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ AdamW */
 /* One AdamW step over n f32 params (reference adamw_fused_kernel,
  * src/kernels_optimizer_impl.inc:11-77) with bias corrections for step
