@@ -63,6 +63,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-bake", action="store_true", help="skip the shadow_bake measurement")
+    ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer measurement")
     ap.add_argument("--cpu-tokens", type=int, default=1536)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (scale for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -189,6 +190,10 @@ def main():
                       "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
     hbm["rope"] = bench_rope(torch, F, sp, p)
     hbm["torch_copy"] = bench_copy(torch)
+    attention = bench_attention(torch, F, sp, p)
+    layer = None
+    if not args.no_layer:
+        layer = bench_layer(torch, F, lib, dev, sp, p, fill, base, sl)
 
     # shadow_bake: 32 layers materialised (config 4)
     bake = None
@@ -220,6 +225,8 @@ def main():
         "hbm_kernels": hbm,
         "cpu_baseline": cpu,
         "bake": bake,
+        "attention": attention,
+        "decoder_layer": layer,
         "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in sorted(kernels.items())},
     }
@@ -250,6 +257,99 @@ def bench_rope(torch, F, sp, p, reps=20):
     nbytes = 2 * 2 * ROPE_B * ROPE_T * (ROPE_HQ + ROPE_HK) * ROPE_HD
     return {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+
+def bench_attention(torch, F, sp, p, reps=10):
+    """Causal GQA attention forward at the decoder-layer shape (q [2,4096,32,128],
+    k/v [2,4096,8,128] bf16); algorithmic work 4*B*Hq*T^2*hd/2 (two causal
+    products)."""
+    bf = torch.bfloat16
+    q = torch.empty((ROPE_B, ROPE_T, ROPE_HQ, ROPE_HD), dtype=bf, device="cuda")
+    k = torch.empty((ROPE_B, ROPE_T, ROPE_HK, ROPE_HD), dtype=bf, device="cuda")
+    v = torch.empty_like(k)
+    o = torch.empty_like(q)
+    for i, t in enumerate((q, k, v)):
+        F.call("glt_fill_normal", p(t), F.DTYPE_BF16, t.numel(), 500, i, 0.0, 1.0, sp)
+
+    def run():
+        F.call("glt_attention_fwd", p(q), p(k), p(v), p(o), ROPE_B, ROPE_T, ROPE_HQ, ROPE_HK, ROPE_HD,
+               ROPE_HD ** -0.5, 1, sp)
+
+    run()
+    torch.cuda.synchronize()
+    F.call("glt_profile_enable", 1)
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    tot, cnt = F.profile_collect().get("attention", (0.0, 1))
+    F.call("glt_profile_enable", 0)
+    t = tot / cnt
+    flop = 4 * ROPE_B * ROPE_HQ * ROPE_T * ROPE_T * ROPE_HD // 2
+    return {"flop": flop, "ms": round(t, 5), "tflops": round(flop / (t * 1e-3) / 1e12, 1),
+            "mfma_frac": round(flop / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+
+
+def bench_layer(torch, F, lib, dev, sp, p, fill, base, sl, reps=5):
+    """Decoder layer with the grafted MLP at 2 x 4096 tokens (hidden 4096, 32
+    query / 8 kv heads of 128, base intermediate 14336, one appended 1024
+    slice): glt_layer_fwd, then the graft-only backward of the MLP with
+    recompute (glt_mlp_bwd); base weights random, the MLP's shared with the
+    MLP step. Work: MLP fwd + bwd as the step's formulas at 8192 tokens,
+    attention projections 2*M*D*(2*q width + 2*kv width), SDPA 4*B*Hq*T^2*hd/2."""
+    bf = torch.bfloat16
+    B, T = ROPE_B, ROPE_T
+    Mt, nq, nk = B * T, ROPE_HQ * ROPE_HD, ROPE_HK * ROPE_HD
+    wq = fill(torch.empty((nq, D), dtype=bf, device=dev), 600, 1, 0.0, 0.02)
+    wk = fill(torch.empty((nk, D), dtype=bf, device=dev), 600, 2, 0.0, 0.02)
+    wv = fill(torch.empty((nk, D), dtype=bf, device=dev), 600, 3, 0.0, 0.02)
+    wo = fill(torch.empty((D, nq), dtype=bf, device=dev), 600, 4, 0.0, 0.02)
+    ln_in = fill(torch.empty(D, dtype=bf, device=dev), 600, 5, 1.0, 0.02)
+    ln_post = fill(torch.empty(D, dtype=bf, device=dev), 600, 6, 1.0, 0.02)
+    x = fill(torch.empty((Mt, D), dtype=bf, device=dev), 600, 7, 0.0, 1.0)
+    dy = fill(torch.empty((Mt, D), dtype=bf, device=dev), 600, 8, 0.0, 1.0)
+    md = F.MlpDesc(Mt, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT, 1, sl, None)
+    ld = F.LayerDesc(B, T, ROPE_HQ, ROPE_HK, ROPE_HD, ROPE_THETA, EPS, md)
+    lw = F.LayerWeights(p(wq), p(wk), p(wv), p(wo), p(ln_in), p(ln_post), None, base)
+    prep = torch.empty(lib.glt_attn_prepared_size(ctypes.byref(ld)), dtype=torch.uint8, device=dev)
+    lw.prepared = prep.data_ptr()
+    F.call("glt_attn_prepare", ctypes.byref(ld), ctypes.byref(lw), p(prep), sp)
+    fws = torch.empty(lib.glt_layer_fwd_workspace_size(ctypes.byref(ld)), dtype=torch.uint8, device=dev)
+    x_ffn = torch.empty_like(x)
+    var = torch.empty(Mt, dtype=torch.float32, device=dev)
+    bd = F.MlpDesc(Mt, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT | F.MLP_RECOMPUTE, 1, sl, None)
+    bws = torch.empty(lib.glt_mlp_bwd_workspace_size(ctypes.byref(bd)), dtype=torch.uint8, device=dev)
+    grads = torch.zeros(3 * S * D, dtype=torch.float32, device=dev)
+    gg = (F.GraftGrads * 1)()
+    gg[0] = F.GraftGrads(grads.data_ptr(), grads.data_ptr() + 4 * S * D, grads.data_ptr() + 8 * S * D)
+
+    def fwd():
+        F.call("glt_layer_fwd", ctypes.byref(ld), ctypes.byref(lw), p(x), p(x_ffn), p(var), None, None, None,
+               p(fws), fws.numel(), sp)
+
+    def bwd():
+        F.call("glt_mlp_bwd", ctypes.byref(bd), ctypes.byref(base), p(x_ffn), p(dy), None, None, None, None, gg,
+               p(bws), bws.numel(), sp)
+
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record()
+    for _ in range(reps):
+        fwd()
+    ev[1].record()
+    for _ in range(reps):
+        bwd()
+    ev[2].record()
+    torch.cuda.synchronize()
+    t_f, t_b = ev[0].elapsed_time(ev[1]) / reps, ev[1].elapsed_time(ev[2]) / reps
+    mlp_flop = STEP_FLOP * Mt // M
+    attn_flop = 2 * Mt * D * (2 * nq + 2 * nk) + 4 * B * ROPE_HQ * T * T * ROPE_HD // 2
+    ms = t_f + t_b
+    return {"workload": "decoder layer (2 x 4096 tokens, 32/8 heads, grafted MLP) fwd + graft-only bwd with recompute",
+            "tokens": Mt, "ms_fwd": round(t_f, 4), "ms_bwd": round(t_b, 4), "ms_step": round(ms, 4),
+            "tokens_per_s": round(Mt / (ms * 1e-3), 1), "algorithmic_flop": mlp_flop + attn_flop,
+            "mfma_frac": round((mlp_flop + attn_flop) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
 
 
 def bench_copy(torch, nbytes=1 << 30, reps=10):
