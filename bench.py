@@ -64,6 +64,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-bake", action="store_true", help="skip the shadow_bake measurement")
     ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer measurement")
+    ap.add_argument("--layer-only", action="store_true",
+                    help="only the attention kernel and decoder-layer measurements (for profiling them alone)")
     ap.add_argument("--cpu-tokens", type=int, default=1536)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (scale for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -136,6 +138,12 @@ def main():
                p(ws), ws_bytes, sp)
         F.call("glt_rmsnorm_bwd", p(dx), p(x_raw), p(gamma), p(var), p(dx_raw), M, D, EPS, sp)
         F.call("glt_adamw_graft_step", sl, 1, gptr, mptr, vptr, pkptr, 7, i, LR, B1, B2, AEPS, WD, sp)
+
+    if args.layer_only:
+        out = {"attention": bench_attention(torch, F, sp, p),
+               "decoder_layer": bench_layer(torch, F, lib, dev, sp, p, fill, base, sl)}
+        print(json.dumps(out), flush=True)
+        return
 
     log("[bench] warmup")
     for i in range(args.warmup):
