@@ -14,7 +14,8 @@ GLT_OK = 0
 STATUS_NAMES = {
     0: "GLT_OK", 1: "GLT_ERR_INVALID_ARG", 2: "GLT_ERR_SHAPE", 3: "GLT_ERR_DTYPE",
     4: "GLT_ERR_ALIGNMENT", 5: "GLT_ERR_WORKSPACE", 6: "GLT_ERR_ALREADY_BAKED",
-    7: "GLT_ERR_BAKED_NO_BACKWARD", 8: "GLT_ERR_HIP", 9: "GLT_ERR_UNSUPPORTED",
+    7: "GLT_ERR_BAKED_NO_BACKWARD", 8: "GLT_ERR_HIP", 9: "GLT_ERR_UNSUPPORTED", 10: "GLT_ERR_IO",
+    11: "GLT_ERR_FORMAT",
 }
 DTYPE_BF16, DTYPE_F32 = 0, 1
 MLP_EXPLICIT, MLP_RECOMPUTE, MLP_RESIDUAL = 1, 2, 4
@@ -57,6 +58,11 @@ class BakeDesc(ctypes.Structure):
                 ("n_slices", _i32), ("placement", ctypes.POINTER(_i32)), ("graft", ctypes.POINTER(_vp))]
 
 
+class GrftInfo(ctypes.Structure):
+    _fields_ = [("num_layers", _i32), ("S", _i32), ("H", _i32), ("hidden_dim", _i32), ("domain_id", _i32),
+                ("session_id", ctypes.c_char_p)]
+
+
 class LayerDesc(ctypes.Structure):
     _fields_ = [("B", _i32), ("T", _i32), ("n_q_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
                 ("rope_theta", _f32), ("rms_eps", _f32), ("mlp", MlpDesc)]
@@ -94,6 +100,9 @@ SIGNATURES = {
     "glt_rmsnorm_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "glt_rope_fwd": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
     "glt_attention_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
+    "glt_grft_save": (_i32, [ctypes.c_char_p, ctypes.POINTER(GrftInfo), _vp, _i32, _vp]),
+    "glt_grft_load": (_i32, [ctypes.c_char_p, ctypes.POINTER(GrftInfo), _vp, _i32, _vp]),
+    "glt_grft_load_raw_f32": (_i32, [ctypes.c_char_p, ctypes.POINTER(GrftInfo), _vp, _i32, _vp]),
     "glt_attn_prepared_size": (_sz, [ctypes.POINTER(LayerDesc)]),
     "glt_attn_prepare": (_i32, [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerWeights), _vp, _vp]),
     "glt_layer_fwd_workspace_size": (_sz, [ctypes.POINTER(LayerDesc)]),

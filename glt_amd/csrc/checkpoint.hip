@@ -1,0 +1,355 @@
+// Graft checkpoint files (host code): the reference's GRFT format
+// (save_safetensors / load_safetensors_checkpoint,
+// src/checkpoint_impl.inc:39-97, :170-285) and its raw f32 --init-deltas
+// file (grafting.hip:882-901).
+//
+// GRFT = u32 magic 0x54465247 | u8 version 4 | safetensors body. The
+// safetensors body is a u64 little-endian header length, a JSON header and
+// the tensor data; its header is parsed here by a small reader of the JSON
+// subset safetensors headers use (objects, arrays, strings, integers).
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace glt {
+
+namespace {
+
+constexpr uint32_t kGrftMagic = 0x54465247u;  // "GRFT"
+constexpr uint8_t kGrftVersion = 4;
+constexpr uint64_t kMaxHeader = 100u << 20;
+
+uint16_t rne_bf16(float f) {
+  uint32_t b;
+  std::memcpy(&b, &f, 4);
+  b += 0x7FFFu + ((b >> 16) & 1u);
+  return (uint16_t)(b >> 16);
+}
+float widen_bf16(uint16_t v) {
+  const uint32_t b = (uint32_t)v << 16;
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+
+// ---- JSON subset reader
+struct JVal {
+  enum Kind { NUL, STR, NUM, OBJ, ARR, BOOL } kind = NUL;
+  std::string str;
+  int64_t num = 0;
+  std::map<std::string, JVal> obj;
+  std::vector<JVal> arr;
+};
+
+struct JParser {
+  const char* p;
+  const char* e;
+  std::string err;
+  void ws() {
+    while (p < e && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p;
+  }
+  bool fail(const char* m) {
+    if (err.empty()) err = m;
+    return false;
+  }
+  bool string(std::string& out) {
+    if (p >= e || *p != '"') return fail("expected a string");
+    ++p;
+    while (p < e && *p != '"') {
+      if (*p == '\\') {
+        if (++p >= e) return fail("bad escape");
+        switch (*p) {
+          case '"': out += '"'; break;
+          case '\\': out += '\\'; break;
+          case '/': out += '/'; break;
+          case 'b': out += '\b'; break;
+          case 'f': out += '\f'; break;
+          case 'n': out += '\n'; break;
+          case 'r': out += '\r'; break;
+          case 't': out += '\t'; break;
+          case 'u': {  // code points below 0x80 only (names and metadata here are ASCII)
+            if (e - p < 5) return fail("bad \\u escape");
+            unsigned v = 0;
+            for (int i = 1; i <= 4; ++i) {
+              const char c = p[i];
+              v = v * 16 + (unsigned)(c >= '0' && c <= '9' ? c - '0' : c >= 'a' && c <= 'f' ? c - 'a' + 10
+                                      : c >= 'A' && c <= 'F' ? c - 'A' + 10 : 255);
+              if (v > 0xFFFF) return fail("bad \\u escape");
+            }
+            if (v >= 0x80) return fail("non-ASCII \\u escape");
+            out += (char)v;
+            p += 4;
+            break;
+          }
+          default: return fail("bad escape");
+        }
+        ++p;
+      } else {
+        out += *p++;
+      }
+    }
+    if (p >= e) return fail("unterminated string");
+    ++p;
+    return true;
+  }
+  bool value(JVal& v, int depth) {
+    if (depth > 16) return fail("nesting too deep");
+    ws();
+    if (p >= e) return fail("unexpected end");
+    if (*p == '{') {
+      v.kind = JVal::OBJ;
+      ++p;
+      ws();
+      if (p < e && *p == '}') return ++p, true;
+      for (;;) {
+        ws();
+        std::string k;
+        if (!string(k)) return false;
+        ws();
+        if (p >= e || *p != ':') return fail("expected ':'");
+        ++p;
+        JVal x;
+        if (!value(x, depth + 1)) return false;
+        v.obj[k] = std::move(x);
+        ws();
+        if (p < e && *p == ',') { ++p; continue; }
+        if (p < e && *p == '}') return ++p, true;
+        return fail("expected ',' or '}'");
+      }
+    }
+    if (*p == '[') {
+      v.kind = JVal::ARR;
+      ++p;
+      ws();
+      if (p < e && *p == ']') return ++p, true;
+      for (;;) {
+        JVal x;
+        if (!value(x, depth + 1)) return false;
+        v.arr.push_back(std::move(x));
+        ws();
+        if (p < e && *p == ',') { ++p; continue; }
+        if (p < e && *p == ']') return ++p, true;
+        return fail("expected ',' or ']'");
+      }
+    }
+    if (*p == '"') {
+      v.kind = JVal::STR;
+      return string(v.str);
+    }
+    if (*p == '-' || (*p >= '0' && *p <= '9')) {
+      v.kind = JVal::NUM;
+      bool neg = *p == '-';
+      if (neg) ++p;
+      if (p >= e || *p < '0' || *p > '9') return fail("bad number");
+      int64_t x = 0;
+      while (p < e && *p >= '0' && *p <= '9') {
+        if (x > (INT64_MAX - 9) / 10) return fail("number too large");
+        x = x * 10 + (*p++ - '0');
+      }
+      if (p < e && (*p == '.' || *p == 'e' || *p == 'E')) return fail("non-integer number");
+      v.num = neg ? -x : x;
+      return true;
+    }
+    auto word = [&](const char* w, JVal::Kind k) {
+      const size_t n = std::strlen(w);
+      if ((size_t)(e - p) < n || std::strncmp(p, w, n) != 0) return fail("bad literal");
+      p += n;
+      v.kind = k;
+      return true;
+    };
+    if (*p == 't') return word("true", JVal::BOOL);
+    if (*p == 'f') return word("false", JVal::BOOL);
+    if (*p == 'n') return word("null", JVal::NUL);
+    return fail("unexpected character");
+  }
+};
+
+bool read_file(const char* path, std::vector<unsigned char>& buf) {
+  FILE* f = std::fopen(path, "rb");
+  if (!f) return false;
+  bool ok = std::fseek(f, 0, SEEK_END) == 0;
+  const long n = ok ? std::ftell(f) : -1;
+  ok = ok && n >= 0 && std::fseek(f, 0, SEEK_SET) == 0;
+  if (ok) {
+    buf.resize((size_t)n);
+    ok = n == 0 || std::fread(buf.data(), 1, (size_t)n, f) == (size_t)n;
+  }
+  std::fclose(f);
+  return ok;
+}
+
+glt_status check_info(const glt_grft_info* d, const char* who) {
+  GLT_CHECK(d, GLT_ERR_INVALID_ARG, "%s: null info", who);
+  GLT_CHECK(d->num_layers > 0 && d->S > 0 && d->H > 0, GLT_ERR_SHAPE, "%s: num_layers=%d S=%d H=%d", who,
+            d->num_layers, d->S, d->H);
+  return GLT_OK;
+}
+
+int64_t n_elems(const glt_grft_info* d) { return (int64_t)d->num_layers * 3 * d->S * d->H; }
+
+// weight <- host f32 values (device: copied on the stream, then waited for)
+glt_status put_weights(float* weight, int on_device, const std::vector<float>& h, hipStream_t st, const char* who) {
+  if (!on_device) {
+    std::memcpy(weight, h.data(), h.size() * 4);
+    return GLT_OK;
+  }
+  GLT_CHECK(hipMemcpyAsync(weight, h.data(), h.size() * 4, hipMemcpyHostToDevice, st) == hipSuccess &&
+                hipStreamSynchronize(st) == hipSuccess,
+            GLT_ERR_HIP, "%s: copy to the device failed", who);
+  return GLT_OK;
+}
+
+}  // namespace
+
+}  // namespace glt
+
+using namespace glt;
+
+extern "C" {
+
+glt_status glt_grft_save(const char* path, const glt_grft_info* info, const float* weight, int32_t weight_on_device,
+                         void* stream) {
+  glt_status s = check_info(info, "glt_grft_save");
+  if (s != GLT_OK) return s;
+  GLT_CHECK(path && weight, GLT_ERR_INVALID_ARG, "glt_grft_save: null path/weight");
+  const int64_t n = n_elems(info);
+  std::vector<float> h((size_t)n);
+  if (weight_on_device) {
+    hipStream_t st = as_stream(stream);
+    GLT_CHECK(hipMemcpyAsync(h.data(), weight, (size_t)n * 4, hipMemcpyDeviceToHost, st) == hipSuccess &&
+                  hipStreamSynchronize(st) == hipSuccess,
+              GLT_ERR_HIP, "glt_grft_save: copy from the device failed");
+  } else {
+    std::memcpy(h.data(), weight, (size_t)n * 4);
+  }
+  std::vector<uint16_t> b((size_t)n);
+  for (int64_t i = 0; i < n; ++i) b[(size_t)i] = rne_bf16(h[(size_t)i]);
+
+  // header in the reference's key order and spelling (src/checkpoint_impl.inc:16-35)
+  const std::string sid = info->session_id ? info->session_id : "";
+  for (char c : sid)
+    GLT_CHECK(c != '"' && c != '\\' && (unsigned char)c >= 0x20, GLT_ERR_INVALID_ARG,
+              "glt_grft_save: session_id needs JSON escaping (not written by the reference format)");
+  const int64_t bytes = n * 2;
+  auto q = [](long long v) { return "\"" + std::to_string(v) + "\""; };
+  std::string header = "{\"__metadata__\":{\"session_id\":\"" + sid + "\",\"domain_id\":" + q(info->domain_id) +
+                       ",\"slice_dim\":" + q(info->S) + ",\"h_slice_dim\":" + q(info->H) +
+                       ",\"hidden_dim\":" + q(info->hidden_dim) + ",\"num_layers\":" + q(info->num_layers) +
+                       "},\"delta_weights\":{\"dtype\":\"BF16\",\"shape\":[" +
+                       std::to_string((long long)info->num_layers * 3) + "," + std::to_string(info->S) + "," +
+                       std::to_string(info->H) + "],\"data_offsets\":[0," + std::to_string((long long)bytes) + "]}}";
+  const uint64_t padded = (header.size() + 7) / 8 * 8;
+
+  FILE* f = std::fopen(path, "wb");
+  GLT_CHECK(f, GLT_ERR_IO, "glt_grft_save: cannot open %s for writing", path);
+  const uint32_t magic = kGrftMagic;
+  const uint8_t ver = kGrftVersion;
+  const std::vector<char> pad(padded - header.size(), '\0');
+  bool ok = std::fwrite(&magic, 4, 1, f) == 1 && std::fwrite(&ver, 1, 1, f) == 1 &&
+            std::fwrite(&padded, 8, 1, f) == 1 && std::fwrite(header.data(), 1, header.size(), f) == header.size() &&
+            (pad.empty() || std::fwrite(pad.data(), 1, pad.size(), f) == pad.size()) &&
+            std::fwrite(b.data(), 2, b.size(), f) == b.size();
+  ok = (std::fclose(f) == 0) && ok;
+  GLT_CHECK(ok, GLT_ERR_IO, "glt_grft_save: short write to %s", path);
+  return GLT_OK;
+}
+
+glt_status glt_grft_load(const char* path, const glt_grft_info* expect, float* weight, int32_t weight_on_device,
+                         void* stream) {
+  glt_status s = check_info(expect, "glt_grft_load");
+  if (s != GLT_OK) return s;
+  GLT_CHECK(path && weight, GLT_ERR_INVALID_ARG, "glt_grft_load: null path/weight");
+  std::vector<unsigned char> buf;
+  GLT_CHECK(read_file(path, buf), GLT_ERR_IO, "glt_grft_load: cannot read %s", path);
+  size_t base = 0;
+  uint32_t magic = 0;
+  if (buf.size() >= 5) std::memcpy(&magic, buf.data(), 4);
+  if (magic == kGrftMagic) base = 5;  // version byte not checked, as the reference (:187-193)
+  GLT_CHECK(buf.size() >= base + 8, GLT_ERR_FORMAT, "glt_grft_load: %s is too short for a header", path);
+  uint64_t hlen = 0;
+  std::memcpy(&hlen, buf.data() + base, 8);
+  GLT_CHECK(hlen <= kMaxHeader && base + 8 + hlen <= buf.size(), GLT_ERR_FORMAT,
+            "glt_grft_load: header length %llu does not fit %s", (unsigned long long)hlen, path);
+  const char* hb = reinterpret_cast<const char*>(buf.data() + base + 8);
+  size_t hn = (size_t)hlen;
+  while (hn > 0 && (hb[hn - 1] == '\0' || hb[hn - 1] == ' ')) --hn;  // NUL (reference) or space padding
+  JParser jp{hb, hb + hn, {}};
+  JVal root;
+  bool ok = jp.value(root, 0);
+  jp.ws();
+  GLT_CHECK(ok && jp.p == jp.e && root.kind == JVal::OBJ, GLT_ERR_FORMAT, "glt_grft_load: bad header in %s: %s",
+            path, jp.err.empty() ? "trailing data" : jp.err.c_str());
+  auto it = root.obj.find("delta_weights");
+  GLT_CHECK(it != root.obj.end() && it->second.kind == JVal::OBJ, GLT_ERR_FORMAT,
+            "glt_grft_load: 'delta_weights' not found in %s", path);
+  const JVal& t = it->second;
+  auto dt = t.obj.find("dtype"), sh = t.obj.find("shape"), off = t.obj.find("data_offsets");
+  GLT_CHECK(dt != t.obj.end() && dt->second.kind == JVal::STR && dt->second.str == "BF16", GLT_ERR_FORMAT,
+            "glt_grft_load: delta_weights dtype is not BF16");
+  const int64_t want[3] = {(int64_t)expect->num_layers * 3, expect->S, expect->H};
+  ok = sh != t.obj.end() && sh->second.kind == JVal::ARR && sh->second.arr.size() == 3;
+  for (int i = 0; ok && i < 3; ++i) ok = sh->second.arr[i].kind == JVal::NUM && sh->second.arr[i].num == want[i];
+  GLT_CHECK(ok, GLT_ERR_FORMAT, "glt_grft_load: delta_weights shape is not [%lld,%lld,%lld]", (long long)want[0],
+            (long long)want[1], (long long)want[2]);
+  const int64_t n = n_elems(expect);
+  const uint64_t data0 = base + 8 + hlen;
+  ok = off != t.obj.end() && off->second.kind == JVal::ARR && off->second.arr.size() == 2 &&
+       off->second.arr[0].kind == JVal::NUM && off->second.arr[1].kind == JVal::NUM;
+  const int64_t b0 = ok ? off->second.arr[0].num : 0, b1 = ok ? off->second.arr[1].num : 0;
+  GLT_CHECK(ok && b0 >= 0 && b1 - b0 == n * 2 && data0 + (uint64_t)b1 <= buf.size(), GLT_ERR_FORMAT,
+            "glt_grft_load: delta_weights data_offsets do not match %lld bf16 values in the file", (long long)n);
+
+  // metadata checks (reference :219-246)
+  std::string file_sid;
+  int64_t file_domain = -1;
+  auto md = root.obj.find("__metadata__");
+  if (md != root.obj.end() && md->second.kind == JVal::OBJ) {
+    auto a = md->second.obj.find("session_id");
+    if (a != md->second.obj.end() && a->second.kind == JVal::STR) file_sid = a->second.str;
+    auto b = md->second.obj.find("domain_id");
+    if (b != md->second.obj.end() && b->second.kind == JVal::STR) {
+      char* endp = nullptr;
+      const long long v = std::strtoll(b->second.str.c_str(), &endp, 10);
+      GLT_CHECK(endp && *endp == '\0' && !b->second.str.empty(), GLT_ERR_FORMAT,
+                "glt_grft_load: domain_id '%s' is not an integer", b->second.str.c_str());
+      file_domain = v;
+    }
+  }
+  const std::string want_sid = expect->session_id ? expect->session_id : "";
+  GLT_CHECK(want_sid.empty() || file_sid.empty() || want_sid == file_sid, GLT_ERR_FORMAT,
+            "glt_grft_load: session_id mismatch (file '%s', expected '%s'): grafts from different training runs "
+            "cannot be mixed", file_sid.c_str(), want_sid.c_str());
+  GLT_CHECK(file_domain == -1 || file_domain == expect->domain_id, GLT_ERR_FORMAT,
+            "glt_grft_load: domain_id mismatch (file %lld, expected %d)", (long long)file_domain,
+            expect->domain_id);
+
+  std::vector<float> h((size_t)n);
+  const unsigned char* src = buf.data() + data0 + b0;
+  for (int64_t i = 0; i < n; ++i) {
+    uint16_t v;
+    std::memcpy(&v, src + 2 * i, 2);
+    h[(size_t)i] = widen_bf16(v);
+  }
+  return put_weights(weight, weight_on_device, h, as_stream(stream), "glt_grft_load");
+}
+
+glt_status glt_grft_load_raw_f32(const char* path, const glt_grft_info* expect, float* weight,
+                                 int32_t weight_on_device, void* stream) {
+  glt_status s = check_info(expect, "glt_grft_load_raw_f32");
+  if (s != GLT_OK) return s;
+  GLT_CHECK(path && weight, GLT_ERR_INVALID_ARG, "glt_grft_load_raw_f32: null path/weight");
+  std::vector<unsigned char> buf;
+  GLT_CHECK(read_file(path, buf), GLT_ERR_IO, "glt_grft_load_raw_f32: cannot read %s", path);
+  const int64_t n = n_elems(expect);
+  GLT_CHECK((int64_t)buf.size() == n * 4, GLT_ERR_FORMAT, "glt_grft_load_raw_f32: %s has %zu bytes, expected %lld",
+            path, buf.size(), (long long)n * 4);
+  std::vector<float> h((size_t)n);
+  std::memcpy(h.data(), buf.data(), buf.size());
+  return put_weights(weight, weight_on_device, h, as_stream(stream), "glt_grft_load_raw_f32");
+}
+
+}  // extern "C"

@@ -296,3 +296,26 @@ class DecoderLayer:
         F.call("glt_layer_fwd", ctypes.byref(self.desc), ctypes.byref(self.weights), _p(x), _p(x_ffn), _p(var),
                None, None, _p(inter), _p(self.ws), self.ws.numel(), _stream())
         return x, x_ffn, var
+
+
+def _grft_info(num_layers, S, H, hidden_dim=0, domain_id=0, session_id=""):
+    return F.GrftInfo(num_layers, S, H, hidden_dim, domain_id, session_id.encode() if session_id else None)
+
+
+def grft_save(path, weight, num_layers, S, H, hidden_dim=0, domain_id=0, session_id=""):
+    """Writes the flat f32 graft storage [num_layers*3*S*H] (device or host
+    tensor) as a GRFT checkpoint (reference save_safetensors,
+    src/checkpoint_impl.inc:39-97)."""
+    info = _grft_info(num_layers, S, H, hidden_dim, domain_id, session_id)
+    F.call("glt_grft_save", str(path).encode(), ctypes.byref(info), _p(weight), int(weight.is_cuda),
+           _stream() if weight.is_cuda else None)
+
+
+def grft_load(path, weight, num_layers, S, H, domain_id=0, session_id="", raw_f32=False):
+    """Loads a GRFT checkpoint (reference load_safetensors_checkpoint,
+    src/checkpoint_impl.inc:170-285) or, with raw_f32, an --init-deltas file
+    into the f32 storage tensor `weight` (device or host)."""
+    info = _grft_info(num_layers, S, H, 0, domain_id, session_id)
+    F.call("glt_grft_load_raw_f32" if raw_f32 else "glt_grft_load", str(path).encode(), ctypes.byref(info),
+           _p(weight), int(weight.is_cuda), _stream() if weight.is_cuda else None)
+    return weight

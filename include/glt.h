@@ -39,6 +39,8 @@ typedef int32_t glt_status;
 #define GLT_ERR_BAKED_NO_BACKWARD  7  /* backward on a shadow-baked model          */
 #define GLT_ERR_HIP                8  /* a HIP runtime call failed                 */
 #define GLT_ERR_UNSUPPORTED        9  /* valid request this build does not serve   */
+#define GLT_ERR_IO                10  /* a file could not be opened, read or written */
+#define GLT_ERR_FORMAT            11  /* file content malformed or not the expected  */
 
 /* ------------------------------------------------------------------ dtypes */
 #define GLT_DTYPE_BF16 0
@@ -327,6 +329,35 @@ size_t glt_layer_fwd_workspace_size(const glt_layer_desc* d);
 glt_status glt_layer_fwd(const glt_layer_desc* d, const glt_layer_weights* w, void* x, void* x_ffn,
                          float* ffn_var, void* gate_pre, void* up_pre, void* inter, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* -------------------------------------------------------- graft checkpoint */
+/* The GRFT graft file (reference save_safetensors / load_safetensors_checkpoint,
+ * src/checkpoint_impl.inc:39-97, :170-285; magic and version
+ * src/checkpoint.hpp:5-6): u32 magic 0x54465247 ("GRFT"), version byte 4, then
+ * a safetensors body: u64 header size, a JSON header padded with NUL bytes to a
+ * multiple of 8, the data. One tensor "delta_weights", BF16 [num_layers*3, S, H]:
+ * the RNE bf16 of the flat f32 graft storage (offset (l*3+p)*S*H, p = gate, up,
+ * down). __metadata__ holds session_id, domain_id, slice_dim, h_slice_dim,
+ * hidden_dim and num_layers as strings. weight_on_device says whether weight
+ * is device memory (copied on stream) or host memory. */
+typedef struct {
+  int32_t num_layers, S, H, hidden_dim, domain_id;
+  const char* session_id; /* nullable = "" */
+} glt_grft_info;
+glt_status glt_grft_save(const char* path, const glt_grft_info* info, const float* weight,
+                         int32_t weight_on_device, void* stream);
+/* Loads delta_weights into the f32 storage (bf16 widened). Accepts files
+ * without the magic (plain safetensors, the reference's legacy form) and
+ * space- or NUL-padded headers. Checks, as the reference: dtype BF16, shape
+ * [num_layers*3, S, H], session_id equal when both are non-empty, domain_id
+ * equal when the file has one (a file without it loads).
+ * GLT_ERR_IO / GLT_ERR_FORMAT on failure; weight is untouched then. */
+glt_status glt_grft_load(const char* path, const glt_grft_info* expect, float* weight,
+                         int32_t weight_on_device, void* stream);
+/* Raw flat f32 storage, the reference's --init-deltas file (grafting.hip:
+ * 882-901): exactly num_layers*3*S*H floats, native byte order. */
+glt_status glt_grft_load_raw_f32(const char* path, const glt_grft_info* expect, float* weight,
+                                 int32_t weight_on_device, void* stream);
 
 /* ------------------------------------------------------------------ AdamW */
 /* One AdamW step over n f32 params (reference adamw_fused_kernel,

@@ -408,3 +408,21 @@ def test_graft_gemm_random_vs_oracle(dev, kind):
     ref = O.graft_gemm(kind, M, S, H, a=a, lda=lda, delta=delta, dy=dy, out=init.copy(), ldo=outshape[1],
                        alpha=0.75, beta=0.5)
     assert_f32_close(to_np(out), ref, tol=1e-5, what=f"kind {kind}")
+
+
+# ------------------------------------------------------------ checkpoint
+def test_grft_checkpoint_device_path(dev, tmp_path):
+    """glt_grft_save / glt_grft_load on device memory: the same file as the
+    host path writes, and the loaded storage equals the RNE bf16 values."""
+    import torch
+    from glt_amd import ops
+    L_, S_, H_ = 3, 64, 96
+    w = np.random.default_rng(9).normal(0, 0.02, L_ * 3 * S_ * H_).astype(np.float32)
+    dpath, hpath = tmp_path / "dev.grft", tmp_path / "host.grft"
+    ops.grft_save(dpath, torch.from_numpy(w).cuda(), L_, S_, H_, hidden_dim=96, domain_id=1, session_id="x")
+    ops.grft_save(hpath, torch.from_numpy(w), L_, S_, H_, hidden_dim=96, domain_id=1, session_id="x")
+    assert dpath.read_bytes() == hpath.read_bytes()
+    out = torch.zeros(L_ * 3 * S_ * H_, device=dev)
+    ops.grft_load(dpath, out, L_, S_, H_, domain_id=1, session_id="x")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), O.f32_to_bf16_bits(w).astype(np.uint32) << 16)
