@@ -122,7 +122,9 @@ __device__ __forceinline__ bool seg_hits(const GSeg& S, const GProb& P, int n0, 
 // A (activations, row-major) goes through LDS: direct-to-LDS buffer loads
 // (buffer_load_dwordx4 ... lds), each wavefront instruction moving 1 KB
 // (8 rows x 128 bytes) with lane L landing at base + 16*L, into a ring of
-// four 32 KB stages, issued three K-steps ahead of use. B (weights) is read
+// four 32 KB stages, issued two to three K-steps ahead of use and spread
+// two per MFMA phase: the CU's address path moves about 64 bytes per clock,
+// and loads issued in a burst stall the issuing wavefronts' MFMAs. B (weights) is read
 // from the shuffled layout of layout.hpp straight into registers: per
 // K-substep a wavefront's four 32-row fragments are four coalesced 1 KB
 // loads, issued one K-step ahead. Rows outside a tile's valid range get an
@@ -165,6 +167,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uni_rsrc(const void* p, uint32
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Workgroup barrier of the K loop: waits for this wavefront's LDS reads
+// (and scalar loads), then s_barrier; the "memory" clobber keeps the
+// compiler from moving memory accesses across it. The caller has already
+// waited for the direct-to-LDS loads the next reads need. __syncthreads()
+// would add a release fence, which the compiler implements by waiting for
+// nearly every direct-to-LDS load in flight, draining the prefetch ring at
+// each barrier.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Orders one wavefront's LDS accesses across lanes: LDS executes a
 // wavefront's instructions in order, so only the compiler must not move
@@ -339,7 +350,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   };
   // MFMAs of substep s (A slot fs) in four groups, one per B fragment j:
   // four MFMAs, then the A read i = j of (rst, rks) into slot fs^1, then the
-  // reload of fb[s][j]; `extra` adds work per group (the phase-3 A loads).
+  // reload of fb[s][j]; `extra` adds work per group (the A loads).
   // The B loads are unconditional: the compiler's waits on fb then stay
   // one K-step deep.
   auto phase = [&](int fs, int s, int rst, int rks, auto&& extra) {
@@ -354,9 +365,9 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  auto no_extra = [](int) {};
 
-  // Pipeline fill: A tiles of K-steps 0..3 into stages 0..3, B of step 0.
+  // Pipeline fill: A tiles of K-steps 0..2 into stages 0..2, loads 0-1 of
+  // step 3 (the rest follow in step 0), B of step 0.
   first_seg(pa);
   pb = pa;
   if (pa.t < total) {
@@ -367,19 +378,21 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
     end_b();
   }
 #pragma unroll 1
-  for (int st = 0; st < kAStages; ++st) {
+  for (int st = 0; st < kAStages - 1; ++st) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) load_a(st, i);
     adv_a();
   }
+  load_a(kAStages - 1, 0);
+  load_a(kAStages - 1, 1);
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int j = 0; j < 4; ++j) load_b(s, j);
   adv_b();
-  // A of step 0: issued first, followed by 24 more A loads and 16 B loads
-  __builtin_amdgcn_s_waitcnt(vmcnt_enc(40));
-  __syncthreads();
+  // A of step 0: issued first, followed by 18 more A loads and 16 B loads
+  __builtin_amdgcn_s_waitcnt(vmcnt_enc(34));
+  ring_barrier();
 #pragma unroll
   for (int i = 0; i < 4; ++i) read_a(0, 0, 0, i);
   int g = 0;  // K-steps consumed so far; step g's A tile sits in stage g % 4
@@ -403,48 +416,56 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
 
     // Per K-step g (A stage st = g % 4):
     //   phases 0-2  MFMAs of substeps 0..2 | A reads of substeps 1..3 |
-    //               B loads of substeps 0..2 of step g+1
+    //               B loads of substeps 0..2 of step g+1 | A loads 2-7 of
+    //               step g+3 into stage (g+3) % 4, free since step g-1
     //   wait for this thread's A loads of step g+1, barrier: step g+1 is in
     //               LDS for everyone and nobody reads stage st any more
-    //   phase 3     MFMAs of substep 3 | A loads of step g+4 into st |
+    //   phase 3     MFMAs of substep 3 | A loads 0-1 of step g+4 into st |
     //               A reads of substep 0 of step g+1 | B loads of substep 3
+    // Every phase issues B, B, A, B, B, A (one B per MFMA group, an A after
+    // groups 1 and 3).
     // Step g+1 may belong to the next tile: its substep-0 A fragments and
     // its B fragments stay in registers across the epilogue.
     for (int it = 0; it < T; ++it, ++g) {
-      const int st = g & (kAStages - 1), nst = (g + 1) & (kAStages - 1);
-      phase(0, 0, st, 1, no_extra);
-      phase(1, 1, st, 2, no_extra);
-      phase(0, 2, st, 3, no_extra);
+      const int st = g & (kAStages - 1), nst = (g + 1) & (kAStages - 1), pst = (g + 3) & (kAStages - 1);
+      phase(0, 0, st, 1, [&](int j) {
+        if (j & 1) load_a(pst, 2 + (j >> 1));
+      });
+      phase(1, 1, st, 2, [&](int j) {
+        if (j & 1) load_a(pst, 4 + (j >> 1));
+      });
+      phase(0, 2, st, 3, [&](int j) {
+        if (j & 1) load_a(pst, 6 + (j >> 1));
+      });
+      adv_a();
       // Loads complete in order, so vmcnt <= n guarantees every load that
-      // has at least n loads issued after it. After the last A load of step
-      // g+1 come 44 loads in step 0 (the fill order) and, from step 1 on,
-      // 60: two whole steps (16 B + 8 A each) and the 12 B loads of phases
-      // 0-2. Stores in between only raise the count. Right after an
-      // epilogue that wait was already done before it, with no stores
-      // outstanding.
+      // has at least n loads issued after it. The last A load of step g+1
+      // was issued at the end of phase 2 of step g-2; after it come 48
+      // loads (phase 3 of step g-2, step g-1, phases 0-2 of step g: 6 per
+      // phase), or 44 in step 0 (the fill order). Stores in between only
+      // raise the count. Right after an epilogue that wait was already done
+      // before it, with no stores outstanding.
       if (prewaited) {
       } else if (g == 0) {
         __builtin_amdgcn_s_waitcnt(vmcnt_enc(44));
       } else {
-        __builtin_amdgcn_s_waitcnt(vmcnt_enc(60));
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(48));
       }
       prewaited = false;
-      __syncthreads();
+      ring_barrier();
       __builtin_amdgcn_sched_barrier(0);
       phase(1, 3, nst, 0, [&](int j) {
-        load_a(st, 2 * j);
-        load_a(st, 2 * j + 1);
+        if (j & 1) load_a(st, j >> 1);
       });
-      adv_a();
       adv_b();
     }
     // The first step of the next tile needs A of step g+1 (g = steps
-    // consumed). Once a step has run, its last load has at least 48 loads
-    // after it (the two steps since), so waiting here, before the
-    // epilogue's stores raise the count, is nearly free. (With no step run
-    // yet only 32 follow it; the first step then waits as usual.)
-    __builtin_amdgcn_s_waitcnt(vmcnt_enc(48));
-    prewaited = g > 0;
+    // consumed). Once two steps have run, its last load has 30 loads after
+    // it (phase 3 of step g-2 and step g-1), so waiting here, before the
+    // epilogue's stores raise the count, is nearly free. (Earlier the first
+    // step waits as usual; the stores only make that wait longer.)
+    if (g >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(30));
+    prewaited = g >= 2;
 
     // ---- epilogue. The B fragment is the MFMA's first operand, so block
     // acc[i][j] is the transposed 32x32 product: lane l owns output row
