@@ -50,6 +50,8 @@ HBM_BYTES = {
     "adamw": S * D * (4 * 4 + 3 * 4),                      # one projection: w, g, m, v in; w, m, v out
 }
 ROPE_B, ROPE_T, ROPE_HQ, ROPE_HK, ROPE_HD, ROPE_THETA = 2, 4096, 32, 8, 128, 500000.0
+# masked cross-entropy bench: 4 x 4096 tokens, Llama-3 vocabulary
+CE_B, CE_T, CE_V = 4, 4096, 128256
 
 
 def log(msg):
@@ -197,6 +199,7 @@ def main():
             hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
                       "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
     hbm["rope"] = bench_rope(torch, F, sp, p)
+    hbm["masked_ce"] = bench_masked_ce(torch, F, sp, p)
     hbm["torch_copy"] = bench_copy(torch)
     attention = bench_attention(torch, F, sp, p)
     layer = None
@@ -265,6 +268,41 @@ def bench_rope(torch, F, sp, p, reps=20):
     nbytes = 2 * 2 * ROPE_B * ROPE_T * (ROPE_HQ + ROPE_HK) * ROPE_HD
     return {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+
+def bench_masked_ce(torch, F, sp, p, reps=5):
+    """Masked cross-entropy + grad_logits over 4 x 4096 tokens of the
+    Llama-3 vocabulary (128256), bf16 logits, every 3rd token excluded;
+    algorithmic bytes: logits read once, gradient written once."""
+    B, T, V = CE_B, CE_T, CE_V
+    bf = torch.bfloat16
+    logits = torch.empty((B, T, V), dtype=bf, device="cuda")
+    grad = torch.empty_like(logits)
+    F.call("glt_fill_normal", p(logits), F.DTYPE_BF16, logits.numel(), 500, 0, 0.0, 3.0, sp)
+    ids = torch.randint(0, V, (B, T), dtype=torch.int32, device="cuda")
+    ood = torch.zeros((B, T), dtype=torch.int32, device="cuda")
+    ood[:, 1::3] = 1
+    stats = torch.empty(4, dtype=torch.float32, device="cuda")
+    nbytes_ws = F.load().glt_masked_ce_workspace_size(B, T)
+    ws = torch.empty(nbytes_ws, dtype=torch.uint8, device="cuda")
+
+    def run():
+        F.call("glt_masked_ce", p(logits), V, p(ids), p(ood), B, T, V, 1.0, p(grad), V, None, p(stats), p(ws),
+               nbytes_ws, sp)
+
+    run()
+    torch.cuda.synchronize()
+    F.call("glt_profile_enable", 1)
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    tot, cnt = F.profile_collect().get("masked_ce", (0.0, 1))
+    F.call("glt_profile_enable", 0)
+    t = tot / cnt
+    nbytes = 2 * 2 * B * T * V
+    del logits, grad
+    return {"bytes": nbytes, "ms": round(t, 4), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "tokens": B * T, "vocab": V}
 
 
 def bench_attention(torch, F, sp, p, reps=10):

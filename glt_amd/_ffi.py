@@ -117,6 +117,13 @@ SIGNATURES = {
     "glt_shadow_bake": (_i32, [ctypes.POINTER(BakeDesc), ctypes.POINTER(ModelState), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), _vp]),
+    "glt_masked_ce_workspace_size": (_sz, [_i32, _i32]),
+    "glt_masked_ce": (_i32, [_vp, _i64, _vp, _vp, _i32, _i32, _i32, ctypes.c_float, _vp, _i64, _vp, _vp, _vp, _sz,
+                             _vp]),
+    "glt_silence_energy": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp, _vp]),
+    "glt_silence_blend": (_i32, [_vp, _vp, _vp, _i32, _i32, ctypes.c_float, _vp]),
+    "glt_silence_blend_energy": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, _vp]),
+    "glt_lr_schedule": (ctypes.c_float, [_i32, _i32, _i32, ctypes.c_float]),
 }
 
 _lib = None

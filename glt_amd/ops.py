@@ -319,3 +319,58 @@ def grft_load(path, weight, num_layers, S, H, domain_id=0, session_id="", raw_f3
     F.call("glt_grft_load_raw_f32" if raw_f32 else "glt_grft_load", str(path).encode(), ctypes.byref(info),
            _p(weight), int(weight.is_cuda), _stream() if weight.is_cuda else None)
     return weight
+
+def masked_ce(logits, ids, ood=None, scale=1.0, grad=None, want_grad=True, ce_per_token=False):
+    """Masked cross-entropy over the shifted logits and its gradient
+    (reference loss grafting.hip:1027-1050, grad_logits :1122-1135).
+    logits [B,T,V] bf16, ids [B,T] int32, ood [B,T] int32 or None.
+    Returns (stats [loss, target-logit mean, target-prob mean, n] f32 on the
+    device, grad [B,T,V] bf16 or None, ce [B*(T-1)] f32 or None). Pass
+    grad=logits to overwrite the logits with the gradient."""
+    B, T, V = logits.shape
+    dev = logits.device
+    stats = torch.empty(4, dtype=torch.float32, device=dev)
+    if want_grad and grad is None:
+        grad = torch.empty_like(logits)
+    ce = torch.empty(max(B * (T - 1), 1), dtype=torch.float32, device=dev) if ce_per_token else None
+    nbytes = F.load().glt_masked_ce_workspace_size(B, T)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    F.call("glt_masked_ce", _p(logits), logits.stride(1), _p(ids), _p(ood), B, T, V, scale,
+           _p(grad) if want_grad else None, grad.stride(1) if want_grad else 0, _p(ce), _p(stats), _p(ws), nbytes,
+           _stream())
+    return stats, (grad if want_grad else None), ce
+
+
+def silence_energy(delta, ld=None):
+    """Per-token energy ||delta_t|| / sqrt(slice) of [tokens, slice] f32 or
+    bf16 rows (reference compute_energy_kernel)."""
+    tokens, slice_ = delta.shape
+    out = torch.empty(tokens, dtype=torch.float32, device=delta.device)
+    dt = F.DTYPE_F32 if delta.dtype == torch.float32 else F.DTYPE_BF16
+    F.call("glt_silence_energy", _p(delta), dt, ld if ld is not None else delta.stride(0), tokens, slice_, _p(out),
+           _stream())
+    return out
+
+
+def silence_blend(dy, delta, ood, lam):
+    """In place: dy += lam * delta / (||delta|| sqrt(slice)) on OOD tokens
+    (reference silence_blend_kernel)."""
+    tokens, slice_ = delta.shape
+    F.call("glt_silence_blend", _p(dy), _p(delta), _p(ood), tokens, slice_, lam, _stream())
+    return dy
+
+
+def silence_blend_energy(dy_gate, delta_gate, dy_up, delta_up, ood, lam, energies=True):
+    """Gate and up silence blend with their energies (reference
+    fused_silence_blend_energy_kernel); returns (energy_gate, energy_up)."""
+    tokens, slice_ = delta_gate.shape
+    eg = torch.empty(tokens, dtype=torch.float32, device=dy_gate.device) if energies else None
+    eu = torch.empty(tokens, dtype=torch.float32, device=dy_gate.device) if energies else None
+    F.call("glt_silence_blend_energy", _p(dy_gate), _p(delta_gate), _p(dy_up), _p(delta_up), _p(eg), _p(eu), _p(ood),
+           tokens, slice_, lam, _stream())
+    return eg, eu
+
+
+def lr_schedule(step, total_steps, warmup_steps, lr_peak):
+    """Warmup + cosine learning rate (reference get_lr, src/config.hpp:122-129)."""
+    return F.load().glt_lr_schedule(step, total_steps, warmup_steps, lr_peak)

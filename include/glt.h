@@ -418,6 +418,50 @@ glt_status glt_shadow_bake(const glt_bake_desc* d, glt_model_state* state,
                            void* const* gate_out, void* const* up_out,
                            void* const* down_out, void* stream);
 
+/* ------------------------------------------------------ training step
+ * Masked cross-entropy over the shifted logits and its gradient: replaces
+ * the reference's ATen loss (grafting.hip:1027-1050) and grad_logits
+ * (:1122-1135). logits: B*T rows of V bf16 at row stride ld (elements);
+ * ids, ood: [B,T] int32 (ood != 0 marks an excluded token). Row (b,t),
+ * t < T-1, is scored against ids[b,t+1] and counts when ood[b,t+1] == 0;
+ * n = max(count, 1). grad (NULL = loss only; may alias logits when
+ * ld_grad == ld) gets B*T rows, row (b,T-1) zero, the others
+ * bf16((bf16(softmax) - onehot)*mask*(1/n)*scale) rounded after every
+ * operation as the reference's bf16 tensor ops do. ce_per_token (NULL or
+ * f32 [B*(T-1)]) gets -bf16(log_softmax[label]). stats (device f32[4]):
+ * loss, mean target logit, mean target probability, n. Labels outside
+ * [0,V) make the row's terms NaN. workspace: glt_masked_ce_workspace_size
+ * bytes, 256-byte aligned. */
+size_t glt_masked_ce_workspace_size(int32_t B, int32_t T);
+glt_status glt_masked_ce(const uint16_t* logits, int64_t ld, const int32_t* ids,
+                         const int32_t* ood, int32_t B, int32_t T, int32_t V,
+                         float scale, uint16_t* grad, int64_t ld_grad,
+                         float* ce_per_token, float* stats, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* OOD silence terms on per-token graft outputs delta [tokens, slice]
+ * (row stride ld): energy[t] = sqrt(sum delta^2 + 1e-8) / sqrt(slice)
+ * (compute_energy_kernel, src/kernels_elementwise_impl.inc:222-275;
+ * dtype GLT_DTYPE_F32 or GLT_DTYPE_BF16, e.g. the graft columns of
+ * gate_pre); glt_silence_blend adds lambda / (||delta|| sqrt(slice)) * delta
+ * to dy for tokens with ood != 0 (silence_blend_kernel, :8-67);
+ * glt_silence_blend_energy does gate and up together, writing both energies
+ * (NULL = skip) and blending tokens with ood == 1
+ * (fused_silence_blend_energy_kernel, :458-560). f32, contiguous rows. */
+glt_status glt_silence_energy(const void* delta, int32_t dtype, int64_t ld, int32_t tokens,
+                              int32_t slice, float* energy, void* stream);
+glt_status glt_silence_blend(float* dy, const float* delta, const int32_t* ood, int32_t tokens,
+                             int32_t slice, float lambda, void* stream);
+glt_status glt_silence_blend_energy(float* dy_gate, const float* delta_gate, float* dy_up,
+                                    const float* delta_up, float* energy_gate, float* energy_up,
+                                    const int32_t* ood, int32_t tokens, int32_t slice,
+                                    float lambda, void* stream);
+
+/* Learning rate of step `step` (0-based) of total_steps: linear warmup to
+ * lr_peak over warmup_steps, then half-cosine decay (get_lr,
+ * src/config.hpp:122-129). Host-only. */
+float glt_lr_schedule(int32_t step, int32_t total_steps, int32_t warmup_steps, float lr_peak);
+
 #ifdef __cplusplus
 }
 #endif

@@ -264,3 +264,97 @@ def mlp_bwd(x, wg, wu, wd, N, slices, g, u, inter, dy, bf16=True, want_dx=True):
     lib().orc_mlp_bwd(M, D, I, N, int(bf16), len(slices), arr, _fp(x), _fp(wg), _fp(wu), _fp(wd), _fp(g), _fp(u),
                       _fp(inter), _fp(dy), _fp(dx), ptrs)
     return dx, grads
+
+
+# --------------------------------------------------- training-step neighbours
+def masked_ce(logits, ids, ood=None, scale=1.0):
+    """Masked cross-entropy over the shifted logits and grad_logits
+    (reference grafting.hip:1027-1050, :1122-1135): row (b, t), t < T-1,
+    against ids[b, t+1], domain mask 1 - ood[b, t+1], n = max(sum mask, 1).
+    Softmax max/sum in float64; every bf16 tensor op of the reference is a
+    bf16 rounding here: p = bf16(softmax), bf16(p - 1) at the label (index_put_),
+    bf16(g * mask), bf16(g * (1/n)) (ATen multiplies by the reciprocal of a
+    scalar divisor), bf16(g * scale); ce = -bf16(x_label - max - log(sum))
+    (log_softmax + gather). Returns (grad [B,T,V] f32 with zero rows at
+    t = T-1, ce [B*(T-1)], stats [loss, mean target logit, mean target prob,
+    n])."""
+    x = np.asarray(logits, np.float32)
+    B, T, V = x.shape
+    R = B * max(T - 1, 0)
+    grad = np.zeros((B, T, V), np.float32)
+    if R == 0:
+        return grad, np.zeros(0, np.float32), np.array([0.0, 0.0, 0.0, 1.0])
+    rows = x[:, :T - 1, :].reshape(R, V).astype(np.float64)
+    lab = np.asarray(ids)[:, 1:].reshape(R).astype(np.int64)
+    mask = (np.ones(R, np.float32) if ood is None
+            else (np.asarray(ood)[:, 1:].reshape(R) == 0).astype(np.float32))
+    n = np.float32(max(float(mask.sum()), 1.0))
+    inv_n = np.float32(1.0) / n
+    m = rows.max(axis=1, keepdims=True)
+    e = np.exp(rows - m)
+    s = e.sum(axis=1, keepdims=True)
+    p = bf16_round((e / s).astype(np.float32))
+    ar = np.arange(R)
+    g = p.copy()
+    g[ar, lab] = bf16_round(g[ar, lab] - np.float32(1.0))
+    g = bf16_round(g * mask[:, None])
+    g = bf16_round(g * inv_n)
+    g = bf16_round(g * np.float32(scale))
+    grad[:, :T - 1, :] = g.reshape(B, T - 1, V)
+    xl = rows[ar, lab]
+    ce = -bf16_round((xl - m[:, 0] - np.log(s[:, 0])).astype(np.float32))
+    pl = p[ar, lab]
+    stats = np.array([(ce.astype(np.float64) * mask).sum() * inv_n,
+                      (xl * mask).sum() * inv_n,
+                      (pl.astype(np.float64) * mask).sum() * inv_n, float(n)])
+    return grad, ce, stats
+
+
+def silence_energy(delta):
+    """||delta_t|| / sqrt(slice) per token row, with the reference's 1e-8
+    inside the root (compute_energy_kernel,
+    src/kernels_elementwise_impl.inc:222-275); float64."""
+    d = np.asarray(delta, np.float64)
+    return np.sqrt((d * d).sum(axis=1) + 1e-8) / np.sqrt(d.shape[1])
+
+
+def silence_blend(dy, delta, ood, lam):
+    """dy + lambda * delta / (||delta|| sqrt(slice)) on rows with ood != 0
+    (silence_blend_kernel, src/kernels_elementwise_impl.inc:8-67)."""
+    d = np.asarray(delta, np.float64)
+    out = np.asarray(dy, np.float64).copy()
+    norm = np.sqrt((d * d).sum(axis=1) + 1e-8)
+    sel = np.asarray(ood) != 0
+    out[sel] += (lam / (norm[sel] * np.sqrt(d.shape[1])))[:, None] * d[sel]
+    return out
+
+
+def silence_blend_energy(dy_g, d_g, dy_u, d_u, ood, lam):
+    """Gate and up (fused_silence_blend_energy_kernel,
+    src/kernels_elementwise_impl.inc:458-560): energies e = ||d|| /
+    sqrt(slice), then on rows with ood == 1 dy += lambda / (e * sqrt(slice)
+    * sqrt(slice) + 1e-8) * d. Returns (dy_g, dy_u, e_g, e_u) in float64."""
+    rs = np.sqrt(np.asarray(d_g).shape[1])
+    outs = []
+    es = []
+    sel = np.asarray(ood) == 1
+    for dy, d in ((dy_g, d_g), (dy_u, d_u)):
+        d = np.asarray(d, np.float64)
+        e = silence_energy(d)
+        o = np.asarray(dy, np.float64).copy()
+        o[sel] += (lam / (e[sel] * rs * rs + 1e-8))[:, None] * d[sel]
+        outs.append(o)
+        es.append(e)
+    return outs[0], outs[1], es[0], es[1]
+
+
+def lr_schedule(step, total_steps, warmup_steps, lr_peak):
+    """Linear warmup then half-cosine decay in float32 arithmetic (get_lr,
+    src/config.hpp:122-129); cos of the float32-rounded argument."""
+    f = np.float32
+    if step < warmup_steps:
+        return f(f(f(lr_peak) * f(step + 1)) / f(warmup_steps))
+    den = f(total_steps - warmup_steps)
+    progress = f(f(step - warmup_steps) / max(den, f(1.0)))
+    c = f(np.cos(np.float64(f(np.pi * np.float64(progress)))))
+    return f(f(f(lr_peak) * f(f(1.0) + c)) * f(0.5))
