@@ -15,9 +15,9 @@ STATUS_NAMES = {
     0: "GLT_OK", 1: "GLT_ERR_INVALID_ARG", 2: "GLT_ERR_SHAPE", 3: "GLT_ERR_DTYPE",
     4: "GLT_ERR_ALIGNMENT", 5: "GLT_ERR_WORKSPACE", 6: "GLT_ERR_ALREADY_BAKED",
     7: "GLT_ERR_BAKED_NO_BACKWARD", 8: "GLT_ERR_HIP", 9: "GLT_ERR_UNSUPPORTED", 10: "GLT_ERR_IO",
-    11: "GLT_ERR_FORMAT",
+    11: "GLT_ERR_FORMAT", 12: "GLT_ERR_NOT_FOUND",
 }
-DTYPE_BF16, DTYPE_F32 = 0, 1
+DTYPE_BF16, DTYPE_F32, DTYPE_F16 = 0, 1, 2
 MLP_EXPLICIT, MLP_RECOMPUTE, MLP_RESIDUAL = 1, 2, 4
 BAKE_IN_PLACE, BAKE_MATERIALIZE = 0, 1
 GEMM_EXPAND_FWD, GEMM_CONTRACT_FWD, GEMM_EXPAND_WGRAD, GEMM_CONTRACT_WGRAD, GEMM_EXPAND_IGRAD, \
@@ -73,6 +73,11 @@ class LayerWeights(ctypes.Structure):
                 ("ln_post", _vp), ("prepared", _vp), ("mlp", BaseWeights)]
 
 
+class LayerBuffers(ctypes.Structure):
+    _fields_ = [("q_proj", _vp), ("k_proj", _vp), ("v_proj", _vp), ("o_proj", _vp), ("ln_in", _vp),
+                ("ln_post", _vp), ("gate", _vp), ("up", _vp), ("down", _vp)]
+
+
 # name -> (restype, argtypes): every entry point declared in include/glt.h
 SIGNATURES = {
     "glt_version": (_i32, []),
@@ -117,6 +122,13 @@ SIGNATURES = {
     "glt_shadow_bake": (_i32, [ctypes.POINTER(BakeDesc), ctypes.POINTER(ModelState), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), _vp]),
+    "glt_st_open": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "glt_st_close": (None, [_vp]),
+    "glt_st_count": (_i32, [_vp]),
+    "glt_st_info": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_i64)]),
+    "glt_st_read": (_i32, [_vp, ctypes.c_char_p, _vp, _i32, _i32, _i32, _vp]),
+    "glt_st_load_layer": (_i32, [_vp, _i32, ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerBuffers), _i32, _vp]),
+    "glt_st_load_head": (_i32, [_vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp]),
     "glt_masked_ce_workspace_size": (_sz, [_i32, _i32]),
     "glt_masked_ce": (_i32, [_vp, _i64, _vp, _vp, _i32, _i32, _i32, ctypes.c_float, _vp, _i64, _vp, _vp, _vp, _sz,
                              _vp]),

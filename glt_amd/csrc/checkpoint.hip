@@ -1,12 +1,21 @@
-// Graft checkpoint files (host code): the reference's GRFT format
+// On-disk formats (host code): the reference's GRFT graft checkpoint
 // (save_safetensors / load_safetensors_checkpoint,
-// src/checkpoint_impl.inc:39-97, :170-285) and its raw f32 --init-deltas
-// file (grafting.hip:882-901).
+// src/checkpoint_impl.inc:39-97, :170-285), its raw f32 --init-deltas file
+// (grafting.hip:882-901) and the base model's safetensors files
+// (load_base_model_safetensors, src/model_io_impl.inc:16-190).
 //
 // GRFT = u32 magic 0x54465247 | u8 version 4 | safetensors body. The
 // safetensors body is a u64 little-endian header length, a JSON header and
 // the tensor data; its header is parsed here by a small reader of the JSON
 // subset safetensors headers use (objects, arrays, strings, integers).
+#include <dirent.h>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -203,8 +212,150 @@ glt_status put_weights(float* weight, int on_device, const std::vector<float>& h
   return GLT_OK;
 }
 
+// ---- base model files
+struct StTensor {
+  int dtype;  // GLT_DTYPE_* or -1 (a dtype this loader does not read)
+  std::vector<int64_t> shape;
+  const unsigned char* data;
+  size_t bytes;
+};
+
+int st_dtype(const std::string& s) {
+  if (s == "BF16") return GLT_DTYPE_BF16;
+  if (s == "F32") return GLT_DTYPE_F32;
+  if (s == "F16") return GLT_DTYPE_F16;
+  return -1;
+}
+size_t st_esize(int dt) { return dt == GLT_DTYPE_F32 ? 4 : 2; }
+
+// IEEE binary16 -> f32 (exact)
+float half_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t ex = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+  uint32_t b;
+  if (ex == 0x1F) {
+    b = sign | 0x7F800000u | (man << 13);
+  } else if (ex != 0) {
+    b = sign | ((ex + 112) << 23) | (man << 13);
+  } else if (man == 0) {
+    b = sign;
+  } else {  // subnormal: renormalise
+    int e = -1;
+    uint32_t m = man;
+    do {
+      ++e;
+      m <<= 1;
+    } while ((m & 0x400u) == 0);
+    b = sign | ((uint32_t)(112 - e) << 23) | ((m & 0x3FFu) << 13);
+  }
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+uint16_t to_bf16(float f) { return std::isnan(f) ? (uint16_t)0x7FC0u : rne_bf16(f); }
+
+float st_elem(const StTensor& t, size_t i) {
+  if (t.dtype == GLT_DTYPE_F32) {
+    float f;
+    std::memcpy(&f, t.data + 4 * i, 4);
+    return f;
+  }
+  uint16_t h;
+  std::memcpy(&h, t.data + 2 * i, 2);
+  return t.dtype == GLT_DTYPE_BF16 ? widen_bf16(h) : half_to_f32(h);
+}
+
 }  // namespace
 
+}  // namespace glt
+
+// the set of mapped files behind a glt_st_set handle
+struct glt_st_set {
+  std::vector<std::pair<void*, size_t>> maps;
+  std::map<std::string, glt::StTensor> tensors;
+};
+
+namespace glt {
+namespace {
+
+void st_unmap(glt_st_set* s) {
+  for (auto& m : s->maps)
+    if (m.first && m.first != MAP_FAILED) munmap(m.first, m.second);
+  s->maps.clear();
+}
+
+// Maps one file and adds its tensors (names already present stay as they are).
+glt_status st_add_file(glt_st_set* s, const std::string& path) {
+  const int fd = open(path.c_str(), O_RDONLY);
+  GLT_CHECK(fd >= 0, GLT_ERR_IO, "glt_st_open: cannot open %s", path.c_str());
+  struct stat stt;
+  const bool st_ok = fstat(fd, &stt) == 0;
+  const size_t size = st_ok ? (size_t)stt.st_size : 0;
+  void* addr = (st_ok && size > 0) ? mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0) : MAP_FAILED;
+  close(fd);
+  GLT_CHECK(st_ok && size >= 8, GLT_ERR_FORMAT, "glt_st_open: %s is not a safetensors file", path.c_str());
+  GLT_CHECK(addr != MAP_FAILED, GLT_ERR_IO, "glt_st_open: cannot map %s", path.c_str());
+  s->maps.emplace_back(addr, size);
+  const unsigned char* base = static_cast<const unsigned char*>(addr);
+  uint64_t hlen = 0;
+  for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | base[i];
+  GLT_CHECK(hlen <= kMaxHeader && hlen <= size - 8, GLT_ERR_FORMAT, "glt_st_open: %s: header length %llu",
+            path.c_str(), (unsigned long long)hlen);
+  JParser jp{reinterpret_cast<const char*>(base + 8), reinterpret_cast<const char*>(base + 8 + hlen), {}};
+  JVal root;
+  GLT_CHECK(jp.value(root, 0) && root.kind == JVal::OBJ, GLT_ERR_FORMAT, "glt_st_open: %s: header: %s",
+            path.c_str(), jp.err.empty() ? "not an object" : jp.err.c_str());
+  const size_t data0 = 8 + (size_t)hlen, avail = size - data0;
+  for (const auto& kv : root.obj) {
+    if (kv.first == "__metadata__") continue;
+    const JVal& t = kv.second;
+    auto dt = t.obj.find("dtype");
+    auto sh = t.obj.find("shape");
+    auto off = t.obj.find("data_offsets");
+    GLT_CHECK(t.kind == JVal::OBJ && dt != t.obj.end() && dt->second.kind == JVal::STR && sh != t.obj.end() &&
+                  sh->second.kind == JVal::ARR && off != t.obj.end() && off->second.kind == JVal::ARR &&
+                  off->second.arr.size() == 2,
+              GLT_ERR_FORMAT, "glt_st_open: %s: tensor %s: malformed entry", path.c_str(), kv.first.c_str());
+    StTensor x;
+    x.dtype = st_dtype(dt->second.str);
+    int64_t n = 1;
+    for (const JVal& d : sh->second.arr) {
+      GLT_CHECK(d.kind == JVal::NUM && d.num >= 0 && (d.num == 0 || n <= INT64_MAX / d.num), GLT_ERR_FORMAT,
+                "glt_st_open: %s: tensor %s: bad shape", path.c_str(), kv.first.c_str());
+      x.shape.push_back(d.num);
+      n *= d.num;
+    }
+    const JVal& b = off->second.arr[0];
+    const JVal& e = off->second.arr[1];
+    GLT_CHECK(b.kind == JVal::NUM && e.kind == JVal::NUM && b.num >= 0 && e.num >= b.num && (size_t)e.num <= avail,
+              GLT_ERR_FORMAT, "glt_st_open: %s: tensor %s: data_offsets outside the file", path.c_str(),
+              kv.first.c_str());
+    x.data = base + data0 + b.num;
+    x.bytes = (size_t)(e.num - b.num);
+    if (x.dtype >= 0)
+      GLT_CHECK(x.bytes == (size_t)n * st_esize(x.dtype), GLT_ERR_FORMAT,
+                "glt_st_open: %s: tensor %s: %zu bytes for %lld elements", path.c_str(), kv.first.c_str(), x.bytes,
+                (long long)n);
+    s->tensors.emplace(kv.first, std::move(x));
+  }
+  return GLT_OK;
+}
+
+const StTensor* st_find(const glt_st_set* s, const char* name) {
+  auto it = s->tensors.find(name);
+  return it == s->tensors.end() ? nullptr : &it->second;
+}
+
+// the tensor's shape, or GLT_ERR_NOT_FOUND / GLT_ERR_SHAPE against `want`
+glt_status st_expect(const glt_st_set* s, const std::string& name, std::vector<int64_t> want, const char* who) {
+  const StTensor* t = st_find(s, name.c_str());
+  GLT_CHECK(t, GLT_ERR_NOT_FOUND, "%s: %s not found", who, name.c_str());
+  GLT_CHECK(t->shape == want, GLT_ERR_SHAPE, "%s: %s has shape of %zu dims, not the expected one", who, name.c_str(),
+            t->shape.size());
+  return GLT_OK;
+}
+
+}  // namespace
 }  // namespace glt
 
 using namespace glt;
@@ -350,6 +501,168 @@ glt_status glt_grft_load_raw_f32(const char* path, const glt_grft_info* expect, 
   std::vector<float> h((size_t)n);
   std::memcpy(h.data(), buf.data(), buf.size());
   return put_weights(weight, weight_on_device, h, as_stream(stream), "glt_grft_load_raw_f32");
+}
+
+glt_status glt_st_open(const char* path, glt_st_set** out) {
+  GLT_CHECK(path && out, GLT_ERR_INVALID_ARG, "glt_st_open: null path/out");
+  *out = nullptr;
+  struct stat st;
+  GLT_CHECK(stat(path, &st) == 0, GLT_ERR_IO, "glt_st_open: %s does not exist", path);
+  std::vector<std::string> files;
+  if (S_ISREG(st.st_mode)) {
+    files.push_back(path);
+  } else if (S_ISDIR(st.st_mode)) {
+    DIR* d = opendir(path);
+    GLT_CHECK(d, GLT_ERR_IO, "glt_st_open: cannot list %s", path);
+    const std::string ext = ".safetensors";
+    for (dirent* e = readdir(d); e; e = readdir(d)) {
+      const std::string n = e->d_name;
+      if (n.size() <= ext.size() || n.compare(n.size() - ext.size(), ext.size(), ext) != 0) continue;
+      const std::string full = std::string(path) + "/" + n;
+      struct stat fs;
+      if (stat(full.c_str(), &fs) == 0 && S_ISREG(fs.st_mode)) files.push_back(full);
+    }
+    closedir(d);
+    std::sort(files.begin(), files.end());
+  }
+  GLT_CHECK(!files.empty(), GLT_ERR_IO, "glt_st_open: no .safetensors files at %s", path);
+  glt_st_set* s = new glt_st_set();
+  for (const std::string& f : files) {
+    const glt_status r = st_add_file(s, f);
+    if (r != GLT_OK) {
+      st_unmap(s);
+      delete s;
+      return r;
+    }
+  }
+  *out = s;
+  return GLT_OK;
+}
+
+void glt_st_close(glt_st_set* s) {
+  if (!s) return;
+  st_unmap(s);
+  delete s;
+}
+
+int32_t glt_st_count(const glt_st_set* s) { return s ? (int32_t)s->tensors.size() : 0; }
+
+glt_status glt_st_info(const glt_st_set* s, const char* name, int32_t* dtype, int32_t* ndim, int64_t* shape) {
+  GLT_CHECK(s && name, GLT_ERR_INVALID_ARG, "glt_st_info: null set/name");
+  const StTensor* t = st_find(s, name);
+  GLT_CHECK(t, GLT_ERR_NOT_FOUND, "glt_st_info: %s not found", name);
+  GLT_CHECK(t->dtype >= 0, GLT_ERR_DTYPE, "glt_st_info: %s has a dtype this loader does not read", name);
+  GLT_CHECK(t->shape.size() <= 8, GLT_ERR_SHAPE, "glt_st_info: %s has %zu dims", name, t->shape.size());
+  if (dtype) *dtype = t->dtype;
+  if (ndim) *ndim = (int32_t)t->shape.size();
+  if (shape)
+    for (size_t i = 0; i < t->shape.size(); ++i) shape[i] = t->shape[i];
+  return GLT_OK;
+}
+
+glt_status glt_st_read(const glt_st_set* s, const char* name, void* dst, int32_t dst_dtype, int32_t transpose,
+                       int32_t on_device, void* stream) {
+  GLT_CHECK(s && name && dst, GLT_ERR_INVALID_ARG, "glt_st_read: null set/name/dst");
+  const StTensor* t = st_find(s, name);
+  GLT_CHECK(t, GLT_ERR_NOT_FOUND, "glt_st_read: %s not found", name);
+  GLT_CHECK(t->dtype >= 0, GLT_ERR_DTYPE, "glt_st_read: %s has a dtype this loader does not read", name);
+  GLT_CHECK(dst_dtype == GLT_DTYPE_BF16 || dst_dtype == GLT_DTYPE_F32, GLT_ERR_DTYPE,
+            "glt_st_read: destination dtype %d", dst_dtype);
+  GLT_CHECK(!transpose || t->shape.size() == 2, GLT_ERR_SHAPE, "glt_st_read: transpose of a %zu-dim tensor",
+            t->shape.size());
+  size_t n = 1;
+  for (int64_t d : t->shape) n *= (size_t)d;
+  const size_t out_bytes = n * st_esize(dst_dtype);
+  const unsigned char* src = t->data;
+  std::vector<unsigned char> stage;
+  if (t->dtype != dst_dtype || (transpose && n > 0)) {
+    stage.resize(out_bytes);
+    const size_t rows = transpose ? (size_t)t->shape[0] : 1, cols = transpose ? (size_t)t->shape[1] : n;
+    for (size_t r = 0; r < rows; ++r)
+      for (size_t c = 0; c < cols; ++c) {
+        const size_t i = r * cols + c, o = transpose ? c * rows + r : i;
+        if (t->dtype == dst_dtype) {
+          std::memcpy(stage.data() + o * st_esize(dst_dtype), t->data + i * st_esize(dst_dtype), st_esize(dst_dtype));
+        } else if (dst_dtype == GLT_DTYPE_BF16) {
+          const uint16_t v = to_bf16(st_elem(*t, i));
+          std::memcpy(stage.data() + 2 * o, &v, 2);
+        } else {
+          const float v = st_elem(*t, i);
+          std::memcpy(stage.data() + 4 * o, &v, 4);
+        }
+      }
+    src = stage.data();
+  }
+  if (out_bytes == 0) return GLT_OK;
+  if (!on_device) {
+    std::memcpy(dst, src, out_bytes);
+    return GLT_OK;
+  }
+  hipStream_t st = as_stream(stream);
+  GLT_CHECK(hipMemcpyAsync(dst, src, out_bytes, hipMemcpyHostToDevice, st) == hipSuccess &&
+                hipStreamSynchronize(st) == hipSuccess,
+            GLT_ERR_HIP, "glt_st_read: copy of %s to the device failed", name);
+  return GLT_OK;
+}
+
+glt_status glt_st_load_layer(const glt_st_set* s, int32_t layer, const glt_layer_desc* d,
+                             const glt_layer_buffers* dst, int32_t on_device, void* stream) {
+  GLT_CHECK(s && d && dst && layer >= 0, GLT_ERR_INVALID_ARG, "glt_st_load_layer: null argument or layer < 0");
+  const int64_t D = d->mlp.D, I = d->mlp.I, nq = (int64_t)d->n_q_heads * d->head_dim,
+                nk = (int64_t)d->n_kv_heads * d->head_dim;
+  const std::string p = "model.layers." + std::to_string(layer) + ".";
+  struct Item {
+    const char* suffix;
+    std::vector<int64_t> shape;
+    void* out;
+  };
+  const Item items[9] = {{"input_layernorm.weight", {D}, dst->ln_in},
+                         {"self_attn.q_proj.weight", {nq, D}, dst->q_proj},
+                         {"self_attn.k_proj.weight", {nk, D}, dst->k_proj},
+                         {"self_attn.v_proj.weight", {nk, D}, dst->v_proj},
+                         {"self_attn.o_proj.weight", {D, nq}, dst->o_proj},
+                         {"post_attention_layernorm.weight", {D}, dst->ln_post},
+                         {"mlp.gate_proj.weight", {I, D}, dst->gate},
+                         {"mlp.up_proj.weight", {I, D}, dst->up},
+                         {"mlp.down_proj.weight", {D, I}, dst->down}};
+  // every tensor is checked before any is copied
+  for (const Item& it : items) {
+    const glt_status r = st_expect(s, p + it.suffix, it.shape, "glt_st_load_layer");
+    if (r != GLT_OK) return r;
+  }
+  for (const Item& it : items) {
+    if (!it.out) continue;
+    const glt_status r = glt_st_read(s, (p + it.suffix).c_str(), it.out, GLT_DTYPE_BF16, 0, on_device, stream);
+    if (r != GLT_OK) return r;
+  }
+  return GLT_OK;
+}
+
+glt_status glt_st_load_head(const glt_st_set* s, int32_t V, int32_t D, void* embed, void* final_norm, void* lm_head,
+                            int32_t on_device, void* stream) {
+  GLT_CHECK(s && V > 0 && D > 0, GLT_ERR_INVALID_ARG, "glt_st_load_head: null set or V/D <= 0");
+  const char* kEmbed = "model.embed_tokens.weight";
+  const char* kNorm = "model.norm.weight";
+  const char* kHead = "lm_head.weight";
+  glt_status r = st_expect(s, kEmbed, {V, D}, "glt_st_load_head");
+  if (r != GLT_OK) return r;
+  if ((r = st_expect(s, kNorm, {D}, "glt_st_load_head")) != GLT_OK) return r;
+  // lm_head: [V,D] as is (also the square case), [D,V] transposed, absent = tied
+  const StTensor* h = st_find(s, kHead);
+  const char* head_src = kEmbed;
+  int transpose = 0;
+  if (h) {
+    const std::vector<int64_t> vd{V, D}, dv{D, V};
+    GLT_CHECK(h->shape == vd || h->shape == dv, GLT_ERR_SHAPE, "glt_st_load_head: lm_head.weight is neither [%d,%d] "
+              "nor [%d,%d]", V, D, D, V);
+    head_src = kHead;
+    transpose = h->shape == vd ? 0 : 1;
+  }
+  if (embed && (r = glt_st_read(s, kEmbed, embed, GLT_DTYPE_BF16, 0, on_device, stream)) != GLT_OK) return r;
+  if (final_norm && (r = glt_st_read(s, kNorm, final_norm, GLT_DTYPE_BF16, 0, on_device, stream)) != GLT_OK) return r;
+  if (lm_head && (r = glt_st_read(s, head_src, lm_head, GLT_DTYPE_BF16, transpose, on_device, stream)) != GLT_OK)
+    return r;
+  return GLT_OK;
 }
 
 }  // extern "C"

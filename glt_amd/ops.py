@@ -374,3 +374,71 @@ def silence_blend_energy(dy_gate, delta_gate, dy_up, delta_up, ood, lam, energie
 def lr_schedule(step, total_steps, warmup_steps, lr_peak):
     """Warmup + cosine learning rate (reference get_lr, src/config.hpp:122-129)."""
     return F.load().glt_lr_schedule(step, total_steps, warmup_steps, lr_peak)
+
+
+class SafetensorsModel:
+    """Base-model weights in safetensors files (reference
+    load_base_model_safetensors, src/model_io_impl.inc:57-190): a file or a
+    directory of *.safetensors, memory-mapped by the library."""
+
+    def __init__(self, path):
+        self._h = ctypes.c_void_p()
+        F.call("glt_st_open", str(path).encode(), ctypes.byref(self._h))
+
+    def close(self):
+        if self._h:
+            F.load().glt_st_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __len__(self):
+        return F.load().glt_st_count(self._h)
+
+    def info(self, name):
+        """(dtype code, shape) of tensor `name`."""
+        dt, nd = ctypes.c_int32(), ctypes.c_int32()
+        shape = (ctypes.c_int64 * 8)()
+        F.call("glt_st_info", self._h, name.encode(), ctypes.byref(dt), ctypes.byref(nd), shape)
+        return dt.value, tuple(shape[i] for i in range(nd.value))
+
+    def read(self, name, dtype=torch.bfloat16, transpose=False, device="cuda"):
+        """Tensor `name` as bf16 or f32, optionally transposed (2-D)."""
+        _, shape = self.info(name)
+        if transpose:
+            shape = shape[::-1]
+        out = torch.empty(shape, dtype=dtype, device=device)
+        on_dev = out.is_cuda
+        F.call("glt_st_read", self._h, name.encode(), _p(out), F.DTYPE_F32 if dtype == torch.float32 else F.DTYPE_BF16,
+               int(transpose), int(on_dev), _stream() if on_dev else None)
+        return out
+
+    def load_layer(self, layer, D, I, n_q_heads, n_kv_heads, head_dim, device="cuda"):
+        """The nine bf16 weights of decoder layer `layer` (names and shapes of
+        the reference's loader); returns a dict."""
+        nq, nk = n_q_heads * head_dim, n_kv_heads * head_dim
+        shapes = {"q_proj": (nq, D), "k_proj": (nk, D), "v_proj": (nk, D), "o_proj": (D, nq), "ln_in": (D,),
+                  "ln_post": (D,), "gate": (I, D), "up": (I, D), "down": (D, I)}
+        out = {k: torch.empty(v, dtype=torch.bfloat16, device=device) for k, v in shapes.items()}
+        bufs = F.LayerBuffers(*[out[k].data_ptr() for k in shapes])
+        md = F.MlpDesc(1, D, I, I, F.DTYPE_BF16, 0, 0, None, None)
+        ld = F.LayerDesc(1, 1, n_q_heads, n_kv_heads, head_dim, 0.0, 1e-5, md)
+        on_dev = torch.device(device).type == "cuda"
+        F.call("glt_st_load_layer", self._h, layer, ctypes.byref(ld), ctypes.byref(bufs), int(on_dev),
+               _stream() if on_dev else None)
+        return out
+
+    def load_head(self, V, D, device="cuda"):
+        """(embed [V,D], final norm [D], lm_head [V,D]) as bf16; lm_head tied
+        to the embedding when the files have none."""
+        embed = torch.empty((V, D), dtype=torch.bfloat16, device=device)
+        norm = torch.empty(D, dtype=torch.bfloat16, device=device)
+        head = torch.empty((V, D), dtype=torch.bfloat16, device=device)
+        on_dev = embed.is_cuda
+        F.call("glt_st_load_head", self._h, V, D, _p(embed), _p(norm), _p(head), int(on_dev),
+               _stream() if on_dev else None)
+        return embed, norm, head

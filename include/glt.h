@@ -41,10 +41,12 @@ typedef int32_t glt_status;
 #define GLT_ERR_UNSUPPORTED        9  /* valid request this build does not serve   */
 #define GLT_ERR_IO                10  /* a file could not be opened, read or written */
 #define GLT_ERR_FORMAT            11  /* file content malformed or not the expected  */
+#define GLT_ERR_NOT_FOUND         12  /* a named tensor is absent from the files     */
 
 /* ------------------------------------------------------------------ dtypes */
 #define GLT_DTYPE_BF16 0
 #define GLT_DTYPE_F32  1
+#define GLT_DTYPE_F16  2  /* stored dtype reported by glt_st_info only */
 
 /* Projection indices, as in the reference flat graft storage
  * (reference src/graft_ops_impl.inc:5-7: offset = (layer*3 + proj)*S*H). */
@@ -417,6 +419,44 @@ glt_status glt_shadow_bake(const glt_bake_desc* d, glt_model_state* state,
                            void* const* gate, void* const* up, void* const* down,
                            void* const* gate_out, void* const* up_out,
                            void* const* down_out, void* stream);
+
+/* ------------------------------------------------------ base model files
+ * Safetensors model weights (reference load_base_model_safetensors /
+ * load_named_tensor / st_to_aten, src/model_io_impl.inc:16-190). path is a
+ * .safetensors file or a directory whose *.safetensors files are used in
+ * sorted order; files are memory-mapped, and a name found in several files
+ * resolves to the first. Stored dtypes BF16, F32, F16 are read; tensors are
+ * delivered as dst_dtype (GLT_DTYPE_BF16 or GLT_DTYPE_F32, RNE on the host),
+ * optionally transposed (2-D only), to device memory on `stream`
+ * (on_device = 1, waited for) or host memory. */
+typedef struct glt_st_set glt_st_set;
+glt_status glt_st_open(const char* path, glt_st_set** out);
+void glt_st_close(glt_st_set* s);
+int32_t glt_st_count(const glt_st_set* s);  /* distinct tensor names */
+/* dtype (GLT_DTYPE_*), ndim and shape (up to 8 dims) of tensor `name`;
+ * GLT_ERR_NOT_FOUND when absent, GLT_ERR_DTYPE for other stored dtypes */
+glt_status glt_st_info(const glt_st_set* s, const char* name, int32_t* dtype, int32_t* ndim,
+                       int64_t* shape);
+glt_status glt_st_read(const glt_st_set* s, const char* name, void* dst, int32_t dst_dtype,
+                       int32_t transpose, int32_t on_device, void* stream);
+/* The nine weights of decoder layer `layer` under the reference's names
+ * (model.layers.{l}.input_layernorm / self_attn.{q,k,v,o}_proj /
+ * post_attention_layernorm / mlp.{gate,up,down}_proj .weight,
+ * src/model_io_impl.inc:104-115), shapes checked against d (q [Hq*hd, D],
+ * k/v [Hkv*hd, D], o [D, Hq*hd], norms [D], gate/up [I, D], down [D, I]),
+ * delivered as bf16. */
+typedef struct {
+  void* q_proj; void* k_proj; void* v_proj; void* o_proj;
+  void* ln_in; void* ln_post;
+  void* gate; void* up; void* down;
+} glt_layer_buffers;
+glt_status glt_st_load_layer(const glt_st_set* s, int32_t layer, const glt_layer_desc* d,
+                             const glt_layer_buffers* dst, int32_t on_device, void* stream);
+/* model.embed_tokens.weight [V,D], model.norm.weight [D] and lm_head.weight
+ * as [V,D] bf16: tied to the embedding when absent, transposed when stored
+ * [D,V], taken as [V,D] when square (src/model_io_impl.inc:118-145). */
+glt_status glt_st_load_head(const glt_st_set* s, int32_t V, int32_t D, void* embed,
+                            void* final_norm, void* lm_head, int32_t on_device, void* stream);
 
 /* ------------------------------------------------------ training step
  * Masked cross-entropy over the shifted logits and its gradient: replaces

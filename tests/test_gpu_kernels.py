@@ -426,3 +426,39 @@ def test_grft_checkpoint_device_path(dev, tmp_path):
     ops.grft_load(dpath, out, L_, S_, H_, domain_id=1, session_id="x")
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), O.f32_to_bf16_bits(w).astype(np.uint32) << 16)
+
+
+def test_safetensors_model_device_path(dev, tmp_path):
+    """glt_st_load_layer / glt_st_load_head / glt_st_read into device memory:
+    the same bits as the host path delivers (stored BF16, F32 and F16)."""
+    import torch
+    from safetensors.torch import save_file
+    from glt_amd import ops
+    D_, I_, hq, hkv, hd, V_ = 64, 96, 4, 2, 16, 80
+    g = torch.Generator().manual_seed(4)
+    p = "model.layers.0."
+    t = {p + "input_layernorm.weight": torch.randn(D_, generator=g),
+         p + "self_attn.q_proj.weight": torch.randn(hq * hd, D_, generator=g).to(torch.bfloat16),
+         p + "self_attn.k_proj.weight": torch.randn(hkv * hd, D_, generator=g).to(torch.float16),
+         p + "self_attn.v_proj.weight": torch.randn(hkv * hd, D_, generator=g).to(torch.bfloat16),
+         p + "self_attn.o_proj.weight": torch.randn(D_, hq * hd, generator=g).to(torch.bfloat16),
+         p + "post_attention_layernorm.weight": torch.randn(D_, generator=g).to(torch.bfloat16),
+         p + "mlp.gate_proj.weight": torch.randn(I_, D_, generator=g).to(torch.bfloat16),
+         p + "mlp.up_proj.weight": torch.randn(I_, D_, generator=g).to(torch.bfloat16),
+         p + "mlp.down_proj.weight": torch.randn(D_, I_, generator=g).to(torch.bfloat16),
+         "model.embed_tokens.weight": torch.randn(V_, D_, generator=g).to(torch.bfloat16),
+         "model.norm.weight": torch.randn(D_, generator=g).to(torch.bfloat16),
+         "lm_head.weight": torch.randn(D_, V_, generator=g).to(torch.bfloat16)}
+    save_file(t, str(tmp_path / "m.safetensors"))
+    with ops.SafetensorsModel(tmp_path / "m.safetensors") as m:
+        wd = m.load_layer(0, D_, I_, hq, hkv, hd, device=dev)
+        wh = m.load_layer(0, D_, I_, hq, hkv, hd, device="cpu")
+        hd_ = m.load_head(V_, D_, device=dev)
+        hh = m.load_head(V_, D_, device="cpu")
+        td = m.read(p + "mlp.down_proj.weight", torch.float32, transpose=True, device=dev)
+        torch.cuda.synchronize()
+        for k in wd:
+            assert torch.equal(wd[k].cpu().view(torch.int16), wh[k].view(torch.int16)), k
+        for a, b in zip(hd_, hh):
+            assert torch.equal(a.cpu(), b)
+        assert torch.equal(td.cpu(), t[p + "mlp.down_proj.weight"].float().t())
