@@ -73,6 +73,17 @@ class LayerWeights(ctypes.Structure):
                 ("ln_post", _vp), ("prepared", _vp), ("mlp", BaseWeights)]
 
 
+class Model(ctypes.Structure):
+    _fields_ = [("num_layers", _i32), ("V", _i32), ("use_explicit_graft", _i32), ("descs", ctypes.POINTER(LayerDesc)),
+                ("layers", ctypes.POINTER(LayerWeights)), ("embed", _vp), ("final_norm", _vp), ("lm_head", _vp),
+                ("lm_head_prepared", _vp)]
+
+
+class EvalResult(ctypes.Structure):
+    _fields_ = [("total_nll", ctypes.c_double), ("count", _i64), ("logits_sum", ctypes.c_double),
+                ("logits_sumsq", ctypes.c_double), ("logits_hash", ctypes.c_uint64)]
+
+
 class LayerBuffers(ctypes.Structure):
     _fields_ = [("q_proj", _vp), ("k_proj", _vp), ("v_proj", _vp), ("o_proj", _vp), ("ln_in", _vp),
                 ("ln_post", _vp), ("gate", _vp), ("up", _vp), ("down", _vp)]
@@ -122,6 +133,14 @@ SIGNATURES = {
     "glt_shadow_bake": (_i32, [ctypes.POINTER(BakeDesc), ctypes.POINTER(ModelState), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), _vp]),
+    "glt_embedding": (_i32, [_vp, _i64, _vp, _i32, _i32, _vp, _vp]),
+    "glt_lm_head_prepared_size": (_sz, [_i32, _i32]),
+    "glt_lm_head_prepare": (_i32, [_vp, _i32, _i32, _vp, _vp]),
+    "glt_lm_head_fwd": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "glt_model_fwd_workspace_size": (_sz, [ctypes.POINTER(Model)]),
+    "glt_model_fwd": (_i32, [ctypes.POINTER(Model), _vp, _vp, _vp, _sz, _vp]),
+    "glt_eval_stats_workspace_size": (_sz, [_i32, _i32]),
+    "glt_eval_stats": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, ctypes.POINTER(EvalResult), _vp, _sz, _vp]),
     "glt_st_open": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "glt_st_close": (None, [_vp]),
     "glt_st_count": (_i32, [_vp]),

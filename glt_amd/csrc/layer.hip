@@ -9,7 +9,9 @@
 //   x   += a . W_o^T                                 MFMA, residual epilogue
 //   x_ffn = rms_norm(x, ln_post)                     glt_rmsnorm_fwd
 //   x   += grafted_mlp(x_ffn)                        glt_mlp_fwd (GLT_MLP_RESIDUAL)
+#include <algorithm>
 #include <cmath>
+#include <vector>
 
 #include "gemm.hpp"
 #include "layout.hpp"
@@ -200,6 +202,217 @@ glt_status glt_layer_fwd(const glt_layer_desc* d, const glt_layer_weights* w, vo
   glt_mlp_desc md = d->mlp;
   md.flags |= GLT_MLP_RESIDUAL;
   return glt_mlp_fwd(&md, &w->mlp, x_ffn, x, gate_pre, up_pre, inter ? inter : ws + L.inter, stream);
+}
+
+}  // extern "C"
+
+// ===================================================================== model
+// forward_model (reference grafting.hip:224-271) and the shadow-eval
+// statistics of its logits (grafting.hip:504-547).
+namespace glt {
+namespace {
+
+// out[t] = table[ids[t]], 16 bytes per lane when rows allow it
+__global__ void __launch_bounds__(256) embedding_kernel(const int32_t* ids, const uint16_t* table, int V, int D,
+                                                        uint16_t* out, bool vec) {
+  const int64_t t = blockIdx.x;
+  const int id = ids[t];
+  const bool ok = id >= 0 && id < V;
+  const uint16_t* src = table + (int64_t)(ok ? id : 0) * D;
+  uint16_t* dst = out + t * D;
+  if (vec) {
+    for (int c = threadIdx.x; c < D / 8; c += 256) {
+      u32x4 v = reinterpret_cast<const u32x4*>(src)[c];
+      if (!ok) v = u32x4{0u, 0u, 0u, 0u};
+      reinterpret_cast<u32x4*>(dst)[c] = v;
+    }
+  } else {
+    for (int c = threadIdx.x; c < D; c += 256) dst[c] = ok ? src[c] : (uint16_t)0;
+  }
+}
+
+// Per-row eval terms, one thread per row, in row order within the row (the
+// hash is sequential): f64 sum / sum of squares of the f32 logits, FNV-1a of
+// their little-endian bytes, and for rows t < T-1 the f32 cross-entropy
+// max + log(sum exp(x - max)) - x_label against ids[b, t+1].
+struct EvalRow {
+  double sum, sumsq;
+  uint64_t hash;
+  float nll;
+  int32_t scored;
+};
+// the reference's offset basis (grafting.hip:505): the published FNV-1a basis
+// 14695981039346656037 with its last digit missing; the hash is defined by it
+constexpr uint64_t kFnvBasis = 1469598103934665603ULL;
+constexpr uint64_t kFnvPrime = 1099511628211ULL;
+
+__global__ void __launch_bounds__(64) eval_rows_kernel(const uint16_t* logits, int64_t ld, const int32_t* ids, int B,
+                                                       int T, int V, EvalRow* rows) {
+  const int64_t r = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (r >= (int64_t)B * T) return;
+  const int b = (int)(r / T), t = (int)(r - (int64_t)b * T);
+  const uint16_t* x = logits + r * ld;
+  double s = 0.0, s2 = 0.0;
+  uint64_t h = kFnvBasis;
+  float mx = -INFINITY;
+  for (int v = 0; v < V; ++v) {
+    const uint32_t bits = (uint32_t)x[v] << 16;
+    const float f = __uint_as_float(bits);
+    s += f;
+    s2 += (double)f * f;
+    mx = fmaxf(mx, f);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      h ^= (bits >> (8 * k)) & 0xFFu;
+      h *= kFnvPrime;
+    }
+  }
+  EvalRow o{s, s2, h, 0.f, 0};
+  if (t < T - 1) {
+    const int label = ids[(int64_t)b * T + t + 1];
+    float se = 0.f;
+    for (int v = 0; v < V; ++v) se += expf(__uint_as_float((uint32_t)x[v] << 16) - mx);
+    const float xl = (label >= 0 && label < V) ? __uint_as_float((uint32_t)x[label] << 16) : NAN;
+    o.nll = (mx + logf(se)) - xl;
+    o.scored = 1;
+  }
+  rows[r] = o;
+}
+
+struct ModelWs {
+  size_t x, x_ffn, var, layer, total;
+};
+ModelWs model_ws(const glt_model* m) {
+  const glt_layer_desc& d0 = m->descs[0];
+  const int64_t M = (int64_t)d0.B * d0.T, D = d0.mlp.D;
+  ModelWs w{};
+  w.x = 0;
+  w.x_ffn = up(w.x + M * D * 2);
+  w.var = up(w.x_ffn + M * D * 2);
+  w.layer = up(w.var + M * 4);
+  size_t lw = 0;
+  for (int l = 0; l < m->num_layers; ++l) lw = std::max(lw, glt_layer_fwd_workspace_size(&m->descs[l]));
+  w.total = up(w.layer + lw);
+  return w;
+}
+
+}  // namespace
+}  // namespace glt
+
+extern "C" {
+
+glt_status glt_embedding(const int32_t* ids, int64_t n, const uint16_t* table, int32_t V, int32_t D, uint16_t* out,
+                         void* stream) {
+  GLT_CHECK(n >= 0 && V > 0 && D > 0, GLT_ERR_SHAPE, "glt_embedding: n=%lld V=%d D=%d", (long long)n, V, D);
+  if (n == 0) return GLT_OK;
+  GLT_CHECK(ids && table && out, GLT_ERR_INVALID_ARG, "glt_embedding: null pointer");
+  const bool vec = D % 8 == 0 && (reinterpret_cast<uintptr_t>(table) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  GLT_LAUNCH("embedding", embedding_kernel, dim3((unsigned)n), dim3(256), 0, as_stream(stream), ids, table, V, D, out,
+             vec);
+  GLT_LAUNCH_CHECK("embedding");
+  return GLT_OK;
+}
+
+size_t glt_lm_head_prepared_size(int32_t V, int32_t D) {
+  return (V > 0 && D > 0) ? (size_t)shuf_elems(V, D) * 2 : 0;
+}
+
+glt_status glt_lm_head_prepare(const uint16_t* lm_head, int32_t V, int32_t D, void* prepared, void* stream) {
+  GLT_CHECK(V > 0 && D > 0, GLT_ERR_SHAPE, "glt_lm_head_prepare: V=%d D=%d", V, D);
+  GLT_CHECK(lm_head && prepared && reinterpret_cast<uintptr_t>(prepared) % kAlign == 0, GLT_ERR_ALIGNMENT,
+            "glt_lm_head_prepare: null pointer or prepared not %zu-byte aligned", kAlign);
+  return shuffle_b(lm_head, GLT_DTYPE_BF16, D, false, V, D, static_cast<uint16_t*>(prepared), as_stream(stream));
+}
+
+glt_status glt_lm_head_fwd(const uint16_t* x, int32_t M, int32_t D, const uint16_t* lm_head, const void* prepared,
+                           int32_t V, uint16_t* logits, void* stream) {
+  GLT_CHECK(M >= 0 && D > 0 && V > 0, GLT_ERR_SHAPE, "glt_lm_head_fwd: M=%d D=%d V=%d", M, D, V);
+  if (M == 0) return GLT_OK;
+  GLT_CHECK(x && lm_head && prepared && logits, GLT_ERR_INVALID_ARG, "glt_lm_head_fwd: null pointer");
+  const Proj p = {lm_head, static_cast<const uint16_t*>(prepared), V, logits};
+  return project(x, M, D, &p, 1, EPI_STORE, "lm_head", as_stream(stream));
+}
+
+size_t glt_model_fwd_workspace_size(const glt_model* m) {
+  return (m && m->num_layers > 0 && m->descs) ? model_ws(m).total : 0;
+}
+
+glt_status glt_model_fwd(const glt_model* m, const int32_t* ids, uint16_t* logits, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  GLT_CHECK(m && m->num_layers > 0 && m->descs && m->layers && m->embed && m->final_norm && m->lm_head &&
+                m->lm_head_prepared && m->V > 0,
+            GLT_ERR_INVALID_ARG, "glt_model_fwd: incomplete model");
+  const glt_layer_desc& d0 = m->descs[0];
+  for (int l = 1; l < m->num_layers; ++l) {
+    const glt_layer_desc& d = m->descs[l];
+    GLT_CHECK(d.B == d0.B && d.T == d0.T && d.mlp.D == d0.mlp.D && d.n_q_heads == d0.n_q_heads &&
+                  d.n_kv_heads == d0.n_kv_heads && d.head_dim == d0.head_dim,
+              GLT_ERR_SHAPE, "glt_model_fwd: layer %d's shape differs from layer 0's", l);
+  }
+  const int64_t M = (int64_t)d0.B * d0.T;
+  const int D = d0.mlp.D;
+  if (M == 0) return GLT_OK;
+  GLT_CHECK(ids && logits, GLT_ERR_INVALID_ARG, "glt_model_fwd: null ids/logits");
+  const ModelWs W = model_ws(m);
+  GLT_CHECK(workspace && workspace_bytes >= W.total && reinterpret_cast<uintptr_t>(workspace) % kAlign == 0,
+            GLT_ERR_WORKSPACE, "glt_model_fwd: needs %zu workspace bytes, %zu-byte aligned", W.total, kAlign);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* x = reinterpret_cast<uint16_t*>(ws + W.x);
+  uint16_t* x_ffn = reinterpret_cast<uint16_t*>(ws + W.x_ffn);
+  float* var = reinterpret_cast<float*>(ws + W.var);
+  glt_status s = glt_embedding(ids, M, m->embed, m->V, D, x, stream);
+  if (s != GLT_OK) return s;
+  for (int l = 0; l < m->num_layers; ++l) {
+    glt_layer_desc d = m->descs[l];
+    d.mlp.flags = m->use_explicit_graft ? (d.mlp.flags | GLT_MLP_EXPLICIT) : (d.mlp.flags & ~GLT_MLP_EXPLICIT);
+    s = glt_layer_fwd(&d, &m->layers[l], x, x_ffn, var, nullptr, nullptr, nullptr, ws + W.layer,
+                      W.total - W.layer, stream);
+    if (s != GLT_OK) return s;
+  }
+  // final norm (into x_ffn) and the LM head
+  s = glt_rmsnorm_fwd(x, m->final_norm, x_ffn, var, (int32_t)M, D, d0.rms_eps, stream);
+  if (s != GLT_OK) return s;
+  return glt_lm_head_fwd(x_ffn, (int32_t)M, D, m->lm_head, m->lm_head_prepared, m->V, logits, stream);
+}
+
+size_t glt_eval_stats_workspace_size(int32_t B, int32_t T) {
+  return (B > 0 && T > 0) ? up((size_t)B * T * sizeof(EvalRow)) : 256;
+}
+
+glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids, int32_t B, int32_t T, int32_t V,
+                          glt_eval_result* out, void* workspace, size_t workspace_bytes, void* stream) {
+  GLT_CHECK(out && B >= 0 && T >= 0 && V > 0 && ld >= V, GLT_ERR_SHAPE, "glt_eval_stats: B=%d T=%d V=%d", B, T, V);
+  *out = glt_eval_result{0.0, 0, 0.0, 0.0, kFnvBasis};
+  const int64_t R = (int64_t)B * T;
+  if (R == 0) return GLT_OK;
+  GLT_CHECK(logits && ids, GLT_ERR_INVALID_ARG, "glt_eval_stats: null logits/ids");
+  GLT_CHECK(workspace && workspace_bytes >= glt_eval_stats_workspace_size(B, T), GLT_ERR_WORKSPACE,
+            "glt_eval_stats: needs %zu workspace bytes", glt_eval_stats_workspace_size(B, T));
+  hipStream_t st = as_stream(stream);
+  EvalRow* rows = static_cast<EvalRow*>(workspace);
+  GLT_LAUNCH("eval_rows", eval_rows_kernel, dim3((unsigned)((R + 63) / 64)), dim3(64), 0, st, logits, ld, ids, B, T,
+             V, rows);
+  GLT_LAUNCH_CHECK("eval_rows");
+  std::vector<EvalRow> h((size_t)R);
+  GLT_CHECK(hipMemcpyAsync(h.data(), rows, (size_t)R * sizeof(EvalRow), hipMemcpyDeviceToHost, st) == hipSuccess &&
+                hipStreamSynchronize(st) == hipSuccess,
+            GLT_ERR_HIP, "glt_eval_stats: copy of the row results failed");
+  uint64_t hash = kFnvBasis;
+  for (const EvalRow& r : h) {
+    out->logits_sum += r.sum;
+    out->logits_sumsq += r.sumsq;
+    if (r.scored) {
+      out->total_nll += r.nll;
+      ++out->count;
+    }
+    for (int k = 0; k < 8; ++k) {
+      hash ^= (r.hash >> (8 * k)) & 0xFFu;
+      hash *= kFnvPrime;
+    }
+  }
+  out->logits_hash = hash;
+  return GLT_OK;
 }
 
 }  // extern "C"

@@ -442,3 +442,85 @@ class SafetensorsModel:
         F.call("glt_st_load_head", self._h, V, D, _p(embed), _p(norm), _p(head), int(on_dev),
                _stream() if on_dev else None)
         return embed, norm, head
+
+
+class Model:
+    """forward_model (reference grafting.hip:224-271) over DecoderLayer
+    objects: embedding, the layers, final RMSNorm, LM head. embed / lm_head
+    [V,D] bf16, final_norm [D] bf16."""
+
+    def __init__(self, layers, embed, final_norm, lm_head=None):
+        self.layers = layers
+        self.embed, self.final_norm = embed, final_norm
+        self.lm_head = embed if lm_head is None else lm_head      # tied when absent
+        self.V, self.D = self.lm_head.shape
+        lib = F.load()
+        self.lm_prepared = torch.empty(lib.glt_lm_head_prepared_size(self.V, self.D), dtype=torch.uint8,
+                                       device=self.lm_head.device)
+        F.call("glt_lm_head_prepare", _p(self.lm_head), self.V, self.D, _p(self.lm_prepared), _stream())
+        n = len(layers)
+        self._descs = (F.LayerDesc * n)(*[l.desc for l in layers])
+        self._weights = (F.LayerWeights * n)(*[l.weights for l in layers])
+
+    def _c(self, explicit):
+        return F.Model(len(self.layers), self.V, int(explicit), self._descs, self._weights, _p(self.embed),
+                       _p(self.final_norm), _p(self.lm_head), _p(self.lm_prepared))
+
+    def forward(self, ids, explicit=True):
+        """ids [B,T] int32 on the device; returns logits [B*T, V] bf16."""
+        m = self._c(explicit)
+        M = ids.numel()
+        logits = torch.empty((M, self.V), dtype=torch.bfloat16, device=ids.device)
+        nbytes = F.load().glt_model_fwd_workspace_size(ctypes.byref(m))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=ids.device)
+        F.call("glt_model_fwd", ctypes.byref(m), _p(ids), _p(logits), _p(ws), nbytes, _stream())
+        return logits
+
+
+def lm_head_fwd(x, lm_head, prepared=None):
+    """logits [M,V] = x [M,D] . lm_head^T (at::linear), bf16."""
+    V, D = lm_head.shape
+    if prepared is None:
+        prepared = torch.empty(F.load().glt_lm_head_prepared_size(V, D), dtype=torch.uint8, device=x.device)
+        F.call("glt_lm_head_prepare", _p(lm_head), V, D, _p(prepared), _stream())
+    out = torch.empty((x.shape[0], V), dtype=torch.bfloat16, device=x.device)
+    F.call("glt_lm_head_fwd", _p(x), x.shape[0], D, _p(lm_head), _p(prepared), V, _p(out), _stream())
+    return out
+
+
+def embedding(ids, table):
+    """table[ids] (at::embedding) for int32 ids, bf16 table [V,D]."""
+    V, D = table.shape
+    out = torch.empty((ids.numel(), D), dtype=torch.bfloat16, device=ids.device)
+    F.call("glt_embedding", _p(ids), ids.numel(), _p(table), V, D, _p(out), _stream())
+    return out
+
+
+def eval_stats(logits, ids):
+    """Shadow-eval terms of one batch (reference grafting.hip:504-547):
+    dict(total_nll, count, ce, logits_sum, logits_sumsq, logits_hash)."""
+    B, T = ids.shape
+    V = logits.shape[-1]
+    lib = F.load()
+    nbytes = lib.glt_eval_stats_workspace_size(B, T)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
+    r = F.EvalResult()
+    F.call("glt_eval_stats", _p(logits), V, _p(ids), B, T, V, ctypes.byref(r), _p(ws), nbytes, _stream())
+    return {"total_nll": r.total_nll, "count": r.count, "ce": r.total_nll / max(r.count, 1),
+            "logits_sum": r.logits_sum, "logits_sumsq": r.logits_sumsq, "logits_hash": r.logits_hash}
+
+
+def certify(A, B, C, D, ce_improve_margin=0.0, eps_ce_bake=0.02, eps_ce_reload=1e-4):
+    """The A/B/C/D gates of the reference's certify step (deploy/certify.sh:28-59;
+    default margins deploy/config.sh:39-41) over eval results (dicts with "ce"
+    and "logits_hash"): A base, B explicit graft, C shadow-baked, D freshly
+    reloaded base."""
+    g1 = B["ce"] < A["ce"] - ce_improve_margin
+    gap = C["ce"] - B["ce"]
+    g2 = abs(gap) < eps_ce_bake
+    g3 = abs(D["ce"] - A["ce"]) < eps_ce_reload and A["logits_hash"] == D["logits_hash"]
+    content = "A_STANDALONE_DELTAS" if (g1 and g2) else ("B_BAKED_MISLABEL_SUSPECT" if g2 else "UNKNOWN")
+    return {"A_ce": A["ce"], "B_ce": B["ce"], "C_ce": C["ce"], "D_ce": D["ce"], "A_hash": A["logits_hash"],
+            "D_hash": D["logits_hash"], "gate_improve": int(g1), "gate_bake_equal": int(g2),
+            "gate_reload_equal": int(g3), "bake_ce_gap": gap, "eps_ce_bake": eps_ce_bake, "content": content,
+            "pass": int(g1 and g2 and g3)}

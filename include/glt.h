@@ -420,6 +420,62 @@ glt_status glt_shadow_bake(const glt_bake_desc* d, glt_model_state* state,
                            void* const* gate_out, void* const* up_out,
                            void* const* down_out, void* stream);
 
+/* ------------------------------------------------------ whole model
+ * forward_model (reference grafting.hip:224-271): embedding, the decoder
+ * layers, final RMSNorm, LM head.
+ * glt_embedding: out[t] = table[ids[t]] (at::embedding), bf16 rows of D;
+ * ids outside [0, V) give zero rows (at::embedding raises).
+ * glt_lm_head_prepare writes lm_head [V,D] in the MFMA fragment layout
+ * (glt_lm_head_prepared_size bytes, 256-byte aligned; once per model);
+ * glt_lm_head_fwd: logits [M,V] = x [M,D] . lm_head^T, bf16 out
+ * (at::linear). */
+glt_status glt_embedding(const int32_t* ids, int64_t n, const uint16_t* table, int32_t V, int32_t D,
+                         uint16_t* out, void* stream);
+size_t glt_lm_head_prepared_size(int32_t V, int32_t D);
+glt_status glt_lm_head_prepare(const uint16_t* lm_head, int32_t V, int32_t D, void* prepared, void* stream);
+glt_status glt_lm_head_fwd(const uint16_t* x, int32_t M, int32_t D, const uint16_t* lm_head,
+                           const void* prepared, int32_t V, uint16_t* logits, void* stream);
+
+/* The whole forward: layers[l] with descs[l] (per-layer graft slices; every
+ * desc has the same B, T, heads and D), use_explicit_graft selects the
+ * graft path of every layer's MLP (the reference's flag; off = base only,
+ * e.g. over shadow-baked weights). logits [B*T, V] bf16. workspace:
+ * glt_model_fwd_workspace_size bytes, 256-byte aligned. */
+typedef struct {
+  int32_t num_layers, V;
+  int32_t use_explicit_graft;
+  const glt_layer_desc* descs;       /* [num_layers] */
+  const glt_layer_weights* layers;   /* [num_layers], attention prepared */
+  const uint16_t* embed;             /* [V,D] */
+  const uint16_t* final_norm;        /* [D] */
+  const uint16_t* lm_head;           /* [V,D] */
+  const void* lm_head_prepared;
+} glt_model;
+size_t glt_model_fwd_workspace_size(const glt_model* m);
+glt_status glt_model_fwd(const glt_model* m, const int32_t* ids, uint16_t* logits, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* Shadow-eval statistics of one logits batch (reference eval loop,
+ * grafting.hip:504-547): over rows (b,t) of B*T bf16 logits (row stride
+ * ld), the f32 cross-entropy of rows t < T-1 against ids[b,t+1] summed in
+ * f64 (total_nll; mean = total_nll / count), the f64 sum and sum of squares
+ * of every logit, and a 64-bit FNV-1a hash: each row's f32 logits hashed
+ * byte by byte (little-endian) from the FNV offset basis, then the row hashes'
+ * 8 bytes chained in row order. (The reference chains every byte of the
+ * batch in one sequence; this form is computed row-parallel, so the value
+ * differs while serving the same purpose: equal logits give equal hashes.)
+ * Synchronous; workspace: glt_eval_stats_workspace_size bytes. */
+typedef struct {
+  double total_nll;
+  int64_t count;
+  double logits_sum, logits_sumsq;
+  uint64_t logits_hash;
+} glt_eval_result;
+size_t glt_eval_stats_workspace_size(int32_t B, int32_t T);
+glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids, int32_t B, int32_t T,
+                          int32_t V, glt_eval_result* out, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* ------------------------------------------------------ base model files
  * Safetensors model weights (reference load_base_model_safetensors /
  * load_named_tensor / st_to_aten, src/model_io_impl.inc:16-190). path is a

@@ -358,3 +358,48 @@ def lr_schedule(step, total_steps, warmup_steps, lr_peak):
     progress = f(f(step - warmup_steps) / max(den, f(1.0)))
     c = f(np.cos(np.float64(f(np.pi * np.float64(progress)))))
     return f(f(f(lr_peak) * f(f(1.0) + c)) * f(0.5))
+
+
+# ---------------------------------------------------------------- model / eval
+# the reference's offset basis (grafting.hip:505) is the published FNV-1a
+# 64-bit basis 14695981039346656037 with its last digit missing; its hash is
+# defined with it, so this one is too
+FNV_BASIS = 1469598103934665603
+FNV_BASIS_PUBLISHED = 14695981039346656037
+FNV_PRIME = 1099511628211
+_M64 = (1 << 64) - 1
+
+
+def fnv1a64(data, h=FNV_BASIS):
+    """64-bit FNV-1a over bytes (the reference's logits hash step,
+    grafting.hip:505, :544-547)."""
+    for b in bytes(data):
+        h = ((h ^ b) * FNV_PRIME) & _M64
+    return h
+
+
+def eval_stats(logits, ids):
+    """Shadow-eval terms (reference grafting.hip:504-547) in this build's
+    row-parallel hash form: each row's f32 logits hashed with FNV-1a, the
+    row hashes' little-endian bytes chained in row order; f64 NLL of rows
+    t < T-1 against ids[b, t+1]; f64 sum and sum of squares."""
+    x = np.asarray(logits, np.float32)
+    B, T = np.asarray(ids).shape
+    V = x.shape[-1]
+    rows = x.reshape(B * T, V)
+    h = FNV_BASIS
+    for r in rows:
+        h = fnv1a64(int(fnv1a64(r.astype("<f4").tobytes())).to_bytes(8, "little"), h)
+    r64 = rows.astype(np.float64)
+    scored = r64.reshape(B, T, V)[:, :T - 1].reshape(-1, V)
+    lab = np.asarray(ids)[:, 1:].reshape(-1)
+    m = scored.max(axis=1)
+    lse = m + np.log(np.exp(scored - m[:, None]).sum(axis=1))
+    nll = lse - scored[np.arange(len(lab)), lab]
+    return {"total_nll": float(nll.sum()), "count": int(nll.size), "logits_sum": float(r64.sum()),
+            "logits_sumsq": float((r64 * r64).sum()), "logits_hash": h}
+
+
+def lm_head(x, w):
+    """logits = bf16(x . w^T) (at::linear on bf16, f64 accumulation here)."""
+    return bf16_round((np.asarray(x, np.float64) @ np.asarray(w, np.float64).T).astype(np.float32))

@@ -1,0 +1,141 @@
+"""GPU parity of the whole-model pieces against the oracle: embedding,
+LM head, forward_model (reference grafting.hip:224-271) with the graft path
+on and off, and the shadow-eval statistics (grafting.hip:504-547)."""
+import numpy as np
+import pytest
+
+from helpers import assert_bf16_budget, draw, make_layer, to_dev, to_np
+from oracle import oracle as O
+from test_gpu_layer import _oracle_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def test_embedding_gathers_rows(dev):
+    import torch
+    from glt_amd import ops
+    V, D = 50, 96
+    table = draw((V, D), 0, 7, 0, 1.0)
+    ids = np.array([0, 49, 3, 3, 17, -1, 50, 8], np.int32)
+    out = ops.embedding(torch.tensor(ids).cuda(), to_dev(table, torch.bfloat16))
+    torch.cuda.synchronize()
+    ref = np.where(((ids >= 0) & (ids < V))[:, None], table[np.clip(ids, 0, V - 1)], 0.0)
+    np.testing.assert_array_equal(to_np(out), ref)
+
+
+@pytest.mark.parametrize("M,D,V", [(100, 256, 1000), (64, 200, 77)])
+def test_lm_head_matches_oracle(dev, M, D, V):
+    import torch
+    from glt_amd import ops
+    x = draw((M, D), 0, 1, 0, 1.0)
+    w = draw((V, D), 0, 2, 0, 0.02)
+    out = ops.lm_head_fwd(to_dev(x, torch.bfloat16), to_dev(w, torch.bfloat16))
+    torch.cuda.synchronize()
+    assert_bf16_budget(to_np(out), O.lm_head(x, w), q=1, what="logits")
+
+
+@pytest.mark.parametrize("explicit", [True, False])
+def test_model_forward_matches_oracle(dev, explicit):
+    import torch
+    from glt_amd import ops
+    bf = torch.bfloat16
+    B, T, D, Hq, Hkv, I, S, V, L = 1, 96, 256, 4, 2, 512, 128, 1000, 2
+    hd, theta, eps = 128, 500000.0, 1e-5
+    N = I + S
+    embed = draw((V, D), 0, 90, 0, 0.05)
+    final_norm = O.bf16_round(1 + draw((D,), 300, 91, 0, 0.02, bf16=False))
+    ids = np.random.default_rng(5).integers(0, V, (B, T)).astype(np.int32)
+    layers, refs = [], []
+    for l in range(L):
+        wq = draw((Hq * hd, D), 0, 30 + 10 * l, 0, 0.02)
+        wk = draw((Hkv * hd, D), 0, 31 + 10 * l, 0, 0.02)
+        wv = draw((Hkv * hd, D), 0, 32 + 10 * l, 0, 0.02)
+        wo = draw((D, Hq * hd), 0, 33 + 10 * l, 0, 0.02)
+        ln_in = O.bf16_round(1 + draw((D,), 300, 12 + 10 * l, 0, 0.02, bf16=False))
+        ln_post = O.bf16_round(1 + draw((D,), 300, 13 + 10 * l, 0, 0.02, bf16=False))
+        wg, wu, wd, sl = make_layer(D, I, N, [(I, S, 0, D)], True, base_seed=100 + l)
+        base = ops.BaseMLP(to_dev(wg, bf), to_dev(wu, bf), to_dev(wd, bf))
+        gs = [ops.GraftSlice(s["i0"], s["s"], s["h0"], s["h"],
+                             *(to_dev(s[p], torch.float32) for p in ("gate", "up", "down"))).pack() for s in sl]
+        layers.append(ops.DecoderLayer(B, T, Hq, Hkv, *(to_dev(w, bf) for w in (wq, wk, wv, wo, ln_in, ln_post)),
+                                       base, gs, N, rope_theta=theta, rms_eps=eps))
+        refs.append((wq, wk, wv, wo, ln_in, ln_post, wg, wu, wd, sl if explicit else []))
+    model = ops.Model(layers, to_dev(embed, bf), to_dev(final_norm, bf))
+    logits = model.forward(torch.tensor(ids).cuda(), explicit=explicit)
+    torch.cuda.synchronize()
+    x = embed[ids.reshape(-1)]
+    for (wq, wk, wv, wo, ln_in, ln_post, wg, wu, wd, sl) in refs:
+        x, _ = _oracle_layer(x, wq, wk, wv, wo, ln_in, ln_post, wg, wu, wd, N, sl, B, T, Hq, Hkv, theta, eps)
+    xn, _ = O.rmsnorm_fwd(x, final_norm, eps)
+    ref = O.lm_head(xn, embed)     # lm_head tied to the embedding
+    assert_bf16_budget(to_np(logits), ref, q=8, what="logits")
+
+
+def test_eval_stats_match_oracle(dev):
+    import torch
+    from glt_amd import ops
+    B, T, V = 2, 33, 1500
+    x = O.bf16_round(np.random.default_rng(8).normal(0, 3, (B * T, V)).astype(np.float32))
+    ids = np.random.default_rng(9).integers(0, V, (B, T)).astype(np.int32)
+    r = ops.eval_stats(to_dev(x, torch.bfloat16), torch.tensor(ids).cuda())
+    ref = O.eval_stats(x.reshape(B, T, V), ids)
+    assert r["logits_hash"] == ref["logits_hash"]
+    assert r["count"] == ref["count"]
+    assert r["total_nll"] == pytest.approx(ref["total_nll"], rel=1e-5)
+    assert r["logits_sum"] == pytest.approx(ref["logits_sum"], rel=1e-9, abs=1e-6)
+    assert r["logits_sumsq"] == pytest.approx(ref["logits_sumsq"], rel=1e-12)
+
+
+def test_certify_bake_and_reload_gates(dev):
+    """The certify run on a two-layer model: A base, B explicit graft, C the
+    shadow-baked weights with the graft path off, D the same base rebuilt.
+    Baked equals explicit within the bake budget (gate 2) and the rebuilt
+    base reproduces A's CE and logits hash (gate 3)."""
+    import torch
+    from glt_amd import _ffi as F
+    from glt_amd import ops
+    bf = torch.bfloat16
+    B, T, D, Hq, Hkv, I, S, V, L = 2, 64, 256, 4, 2, 512, 128, 1000, 2
+    N = I + S
+    embed = to_dev(draw((V, D), 0, 90, 0, 0.05), bf)
+    final_norm = to_dev(O.bf16_round(1 + draw((D,), 300, 91, 0, 0.02, bf16=False)), bf)
+    ids = torch.tensor(np.random.default_rng(6).integers(0, V, (B, T)).astype(np.int32)).cuda()
+    att, mlp = [], []
+    for l in range(L):
+        att.append([to_dev(draw(sh, 0, 40 + 10 * l + k, 0, 0.02), bf) for k, sh in
+                    enumerate(((Hq * 128, D), (Hkv * 128, D), (Hkv * 128, D), (D, Hq * 128)))] +
+                   [to_dev(O.bf16_round(1 + draw((D,), 300, 44 + 10 * l + k, 0, 0.02, bf16=False)), bf)
+                    for k in range(2)])
+        wg, wu, wd, sl = make_layer(D, I, N, [(I, S, 0, D)], True, base_seed=200 + l, graft_std=0.05)
+        gs = [ops.GraftSlice(s["i0"], s["s"], s["h0"], s["h"],
+                             *(to_dev(s[p], torch.float32) for p in ("gate", "up", "down"))).pack() for s in sl]
+        mlp.append((to_dev(wg, bf), to_dev(wu, bf), to_dev(wd, bf), gs))
+
+    def model(bases, slices):
+        layers = [ops.DecoderLayer(B, T, Hq, Hkv, *att[l], bases[l], slices[l], N) for l in range(L)]
+        return ops.Model(layers, embed, final_norm)
+
+    def ev(m, explicit):
+        return ops.eval_stats(m.forward(ids, explicit=explicit), ids)
+
+    bases = [ops.BaseMLP(wg, wu, wd) for (wg, wu, wd, _) in mlp]
+    m = model(bases, [gs for (_, _, _, gs) in mlp])
+    A, Bx = ev(m, False), ev(m, True)
+    baked = []
+    for (wg, wu, wd, gs) in mlp:
+        go = torch.empty((N, D), dtype=bf, device="cuda")
+        uo = torch.empty((N, D), dtype=bf, device="cuda")
+        do = torch.empty((D, N), dtype=bf, device="cuda")
+        flat = [[torch.cat([s.gate.reshape(-1), s.up.reshape(-1), s.down.reshape(-1)])] for s in gs]
+        ops.shadow_bake(F.ModelState(0), [wg], [wu], [wd], flat, [(s.i_start, s.s, s.h_start, s.h) for s in gs],
+                        D=D, I=I, N=N, materialize=True, gate_out=[go], up_out=[uo], down_out=[do])
+        baked.append(ops.BaseMLP(go, uo, do))
+    C = ev(model(baked, [[] for _ in range(L)]), False)
+    Dr = ev(model([ops.BaseMLP(wg, wu, wd) for (wg, wu, wd, _) in mlp], [[] for _ in range(L)]), False)
+    torch.cuda.synchronize()
+    r = ops.certify(A, Bx, C, Dr)
+    print({k: r[k] for k in ("A_ce", "B_ce", "C_ce", "D_ce", "bake_ce_gap")}, flush=True)
+    assert Bx["ce"] != A["ce"]                 # the graft changes the model
+    assert r["gate_bake_equal"] == 1, r
+    assert r["gate_reload_equal"] == 1, r
+    assert abs(r["bake_ce_gap"]) < 2e-3

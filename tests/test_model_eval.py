@@ -1,0 +1,61 @@
+"""Model-level pieces on the CPU: the FNV-1a hash pinned to its published
+test vectors, the eval oracle's cross-entropy pinned to torch's
+cross_entropy as the reference calls it (grafting.hip:527-532), and the
+certify gates (deploy/certify.sh:28-59)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+def test_fnv1a64_known_answers():
+    # published FNV-1a 64-bit test vectors (with the published basis)
+    h0 = O.FNV_BASIS_PUBLISHED
+    assert O.fnv1a64(b"", h0) == 0xcbf29ce484222325
+    assert O.fnv1a64(b"a", h0) == 0xaf63dc4c8601ec8c
+    assert O.fnv1a64(b"foobar", h0) == 0x85944171f73967e8
+    # the reference's basis constant (grafting.hip:505) is that number with
+    # its last digit dropped; the eval hash starts from it
+    assert O.FNV_BASIS == O.FNV_BASIS_PUBLISHED // 10 and O.fnv1a64(b"") == O.FNV_BASIS
+
+
+def test_eval_oracle_ce_matches_torch_cross_entropy():
+    rng = np.random.default_rng(1)
+    B, T, V = 3, 7, 300
+    x = O.bf16_round(rng.normal(0, 4, (B, T, V)).astype(np.float32))
+    ids = rng.integers(0, V, (B, T)).astype(np.int32)
+    st = O.eval_stats(x, ids)
+    lt = torch.tensor(x)[:, :T - 1].permute(0, 2, 1).contiguous()
+    ce = torch.nn.functional.cross_entropy(lt, torch.tensor(ids[:, 1:].astype(np.int64)), reduction="mean")
+    assert st["count"] == B * (T - 1)
+    assert st["total_nll"] / st["count"] == pytest.approx(ce.item(), rel=1e-6)
+    assert st["logits_sum"] == pytest.approx(float(x.astype(np.float64).sum()), rel=1e-12)
+
+
+def test_eval_hash_is_order_and_value_sensitive():
+    rng = np.random.default_rng(2)
+    x = O.bf16_round(rng.normal(0, 1, (1, 4, 16)).astype(np.float32))
+    ids = np.zeros((1, 4), np.int32)
+    h = O.eval_stats(x, ids)["logits_hash"]
+    y = x.copy()
+    y[0, 2, 5] = np.nextafter(y[0, 2, 5], np.float32(np.inf))
+    assert O.eval_stats(y, ids)["logits_hash"] != h
+    z = x[:, ::-1].copy()
+    assert O.eval_stats(z, ids)["logits_hash"] != h
+    # one row: FNV-1a of the row's bytes, then of that hash's 8 bytes
+    r = O.eval_stats(x[:, :1], ids[:, :1])["logits_hash"]
+    assert r == O.fnv1a64(O.fnv1a64(x[0, 0].astype("<f4").tobytes()).to_bytes(8, "little"))
+
+
+def test_certify_gates():
+    from glt_amd import ops
+    A = {"ce": 2.0, "logits_hash": 7}
+    B = {"ce": 1.5, "logits_hash": 8}
+    C = {"ce": 1.51, "logits_hash": 9}
+    r = ops.certify(A, B, C, dict(A))
+    assert r["pass"] == 1 and r["content"] == "A_STANDALONE_DELTAS"
+    assert ops.certify(A, B, {"ce": 1.6, "logits_hash": 9}, dict(A))["gate_bake_equal"] == 0
+    assert ops.certify(A, {"ce": 2.0, "logits_hash": 8}, {"ce": 2.0, "logits_hash": 9}, dict(A))["content"] == \
+        "B_BAKED_MISLABEL_SUSPECT"
+    assert ops.certify(A, B, C, {"ce": 2.0, "logits_hash": 6})["gate_reload_equal"] == 0
