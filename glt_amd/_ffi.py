@@ -137,6 +137,7 @@ SIGNATURES = {
     "glt_lm_head_prepared_size": (_sz, [_i32, _i32]),
     "glt_lm_head_prepare": (_i32, [_vp, _i32, _i32, _vp, _vp]),
     "glt_lm_head_fwd": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "glt_lm_head_bwd": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
     "glt_model_fwd_workspace_size": (_sz, [ctypes.POINTER(Model)]),
     "glt_model_fwd": (_i32, [ctypes.POINTER(Model), _vp, _vp, _vp, _sz, _vp]),
     "glt_eval_stats_workspace_size": (_sz, [_i32, _i32]),

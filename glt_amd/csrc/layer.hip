@@ -314,15 +314,50 @@ glt_status glt_embedding(const int32_t* ids, int64_t n, const uint16_t* table, i
   return GLT_OK;
 }
 
+// prepared LM head: [V rows, K = D] (forward), then 256-byte aligned the
+// transpose [D rows, K = V] (backward), both in the fragment layout
+size_t lm_head_t_offset(int32_t V, int32_t D) { return up((size_t)shuf_elems(V, D) * 2); }
+
 size_t glt_lm_head_prepared_size(int32_t V, int32_t D) {
-  return (V > 0 && D > 0) ? (size_t)shuf_elems(V, D) * 2 : 0;
+  return (V > 0 && D > 0) ? lm_head_t_offset(V, D) + (size_t)shuf_elems(D, V) * 2 : 0;
 }
 
 glt_status glt_lm_head_prepare(const uint16_t* lm_head, int32_t V, int32_t D, void* prepared, void* stream) {
   GLT_CHECK(V > 0 && D > 0, GLT_ERR_SHAPE, "glt_lm_head_prepare: V=%d D=%d", V, D);
   GLT_CHECK(lm_head && prepared && reinterpret_cast<uintptr_t>(prepared) % kAlign == 0, GLT_ERR_ALIGNMENT,
             "glt_lm_head_prepare: null pointer or prepared not %zu-byte aligned", kAlign);
-  return shuffle_b(lm_head, GLT_DTYPE_BF16, D, false, V, D, static_cast<uint16_t*>(prepared), as_stream(stream));
+  hipStream_t st = as_stream(stream);
+  uint16_t* p = static_cast<uint16_t*>(prepared);
+  glt_status s = shuffle_b(lm_head, GLT_DTYPE_BF16, D, false, V, D, p, st);
+  if (s != GLT_OK) return s;
+  return shuffle_b(lm_head, GLT_DTYPE_BF16, D, true, D, V, p + lm_head_t_offset(V, D) / 2, st);
+}
+
+glt_status glt_lm_head_bwd(const uint16_t* grad, int32_t M, int32_t V, const uint16_t* lm_head, const void* prepared,
+                           int32_t D, float* dx, void* stream) {
+  GLT_CHECK(M >= 0 && D > 0 && V > 0, GLT_ERR_SHAPE, "glt_lm_head_bwd: M=%d D=%d V=%d", M, D, V);
+  if (M == 0) return GLT_OK;
+  GLT_CHECK(grad && lm_head && prepared && dx, GLT_ERR_INVALID_ARG, "glt_lm_head_bwd: null pointer");
+  // dx[m, d] = sum_v grad[m, v] lm_head[v, d]: B(n = d, k = v) = lm_head^T
+  const uint16_t* pt = static_cast<const uint16_t*>(prepared) + lm_head_t_offset(V, D) / 2;
+  GemmPlan plan;
+  plan.label = "lm_head_bwd";
+  plan.a_kind = LD_BF16;
+  plan.b_kind = LD_SHUF;
+  GProb pr = prob(M, D, EPI_STORE, dx);
+  pr.out_f32 = 1;
+  plan.add_problem(pr);
+  plan.add_seg(seg(grad, V, V, D, pt, shuf_k(V)));
+  hipStream_t st = as_stream(stream);
+  if (gemm_mfma_eligible(plan)) return run_gemm(plan, st);
+  GemmPlan gen;
+  gen.label = "lm_head_bwd";
+  gen.a_kind = gen.b_kind = LD_BF16;
+  gen.add_problem(pr);
+  GSeg g = seg(grad, V, V, D, lm_head, 1);
+  g.b_ks = D;  // B(n = d, k = v) = lm_head[v * D + d]
+  gen.add_seg(g);
+  return run_gemm(gen, st, false);
 }
 
 glt_status glt_lm_head_fwd(const uint16_t* x, int32_t M, int32_t D, const uint16_t* lm_head, const void* prepared,

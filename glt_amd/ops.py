@@ -488,6 +488,18 @@ def lm_head_fwd(x, lm_head, prepared=None):
     return out
 
 
+def lm_head_bwd(grad, lm_head, prepared=None):
+    """dx [M,D] f32 = grad [M,V] . lm_head (the reference's grad_logits_full @
+    lm_head, grafting.hip:1137)."""
+    V, D = lm_head.shape
+    if prepared is None:
+        prepared = torch.empty(F.load().glt_lm_head_prepared_size(V, D), dtype=torch.uint8, device=grad.device)
+        F.call("glt_lm_head_prepare", _p(lm_head), V, D, _p(prepared), _stream())
+    dx = torch.empty((grad.shape[0], D), dtype=torch.float32, device=grad.device)
+    F.call("glt_lm_head_bwd", _p(grad), grad.shape[0], V, _p(lm_head), _p(prepared), D, _p(dx), _stream())
+    return dx
+
+
 def embedding(ids, table):
     """table[ids] (at::embedding) for int32 ids, bf16 table [V,D]."""
     V, D = table.shape

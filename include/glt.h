@@ -425,16 +425,19 @@ glt_status glt_shadow_bake(const glt_bake_desc* d, glt_model_state* state,
  * layers, final RMSNorm, LM head.
  * glt_embedding: out[t] = table[ids[t]] (at::embedding), bf16 rows of D;
  * ids outside [0, V) give zero rows (at::embedding raises).
- * glt_lm_head_prepare writes lm_head [V,D] in the MFMA fragment layout
- * (glt_lm_head_prepared_size bytes, 256-byte aligned; once per model);
- * glt_lm_head_fwd: logits [M,V] = x [M,D] . lm_head^T, bf16 out
- * (at::linear). */
+ * glt_lm_head_prepare writes lm_head [V,D] and its transpose in the MFMA
+ * fragment layout (glt_lm_head_prepared_size bytes, 256-byte aligned; once
+ * per model); glt_lm_head_fwd: logits [M,V] = x [M,D] . lm_head^T, bf16 out
+ * (at::linear); glt_lm_head_bwd: dx [M,D] = grad [M,V] . lm_head, f32 out
+ * (the reference's dx = grad_logits_full @ lm_head, grafting.hip:1137). */
 glt_status glt_embedding(const int32_t* ids, int64_t n, const uint16_t* table, int32_t V, int32_t D,
                          uint16_t* out, void* stream);
 size_t glt_lm_head_prepared_size(int32_t V, int32_t D);
 glt_status glt_lm_head_prepare(const uint16_t* lm_head, int32_t V, int32_t D, void* prepared, void* stream);
 glt_status glt_lm_head_fwd(const uint16_t* x, int32_t M, int32_t D, const uint16_t* lm_head,
                            const void* prepared, int32_t V, uint16_t* logits, void* stream);
+glt_status glt_lm_head_bwd(const uint16_t* grad, int32_t M, int32_t V, const uint16_t* lm_head,
+                           const void* prepared, int32_t D, float* dx, void* stream);
 
 /* The whole forward: layers[l] with descs[l] (per-layer graft slices; every
  * desc has the same B, T, heads and D), use_explicit_graft selects the
