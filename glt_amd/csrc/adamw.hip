@@ -34,7 +34,17 @@ __device__ __forceinline__ float clip_scale(const float* partial, int np, float 
   return norm > clip ? clip / norm : 1.0f;
 }
 
-// (reference adamw_fused_kernel, src/kernels_optimizer_impl.inc:27-51)
+// One AdamW element update in the reference's operation order
+// (reference adamw_fused_kernel, src/kernels_optimizer_impl.inc:27-51).
+__device__ __forceinline__ float adamw_elem(float wi, float gi, float& mi, float& vi, float lr, float b1, float b2,
+                                            float b1c, float b2c, float eps, float wd) {
+  mi = b1 * mi + (1.0f - b1) * gi;
+  vi = b2 * vi + (1.0f - b2) * gi * gi;
+  const float mh = mi * b1c, vh = vi * b2c;
+  const float denom = sqrtf(vh) + eps;
+  return wi - lr * mh / denom - lr * wd * wi;
+}
+
 __global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ w, const float* __restrict__ g,
                                                     float* __restrict__ m, float* __restrict__ v,
                                                     uint16_t* __restrict__ mirror, int64_t n, float lr,
@@ -49,20 +59,95 @@ __global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ w, const
   const float scale = partial ? s_scale : 1.0f;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const float gi = g[i] * scale;
     float mi = m[i], vi = v[i];
-    mi = b1 * mi + (1.0f - b1) * gi;
-    vi = b2 * vi + (1.0f - b2) * gi * gi;
+    const float nw = adamw_elem(w[i], g[i] * scale, mi, vi, lr, b1, b2, b1c, b2c, eps, wd);
     m[i] = mi;
     v[i] = vi;
-    const float mh = mi * b1c, vh = vi * b2c;
-    const float denom = sqrtf(vh) + eps;
-    const float wi = w[i];
-    const float nw = wi - lr * mh / denom - lr * wd * wi;
     w[i] = nw;
     if (mirror) mirror[i] = f32_to_bf16(nw);
   }
 }
+
+// AdamW over one [S, H] graft projection fused with the refresh of its four
+// bf16 mirrors in the packed slice: row-major [S,H], row-major [H,S], and
+// the fragment layout of both. One workgroup per 64 x 64 tile (S and H
+// multiples of 64, so no fragment block is padded): the f32 state streams
+// through registers as 16-byte accesses, the new weights go through LDS
+// once, and every mirror is written with 16-byte stores. The master is read
+// once instead of once per mirror.
+__global__ void __launch_bounds__(256) adamw_pack_kernel(float* __restrict__ w, const float* __restrict__ g,
+                                                         float* __restrict__ m, float* __restrict__ v, int S,
+                                                         int H, float lr, float b1, float b2, float b1c,
+                                                         float b2c, float eps, float wd,
+                                                         uint16_t* __restrict__ rm, uint16_t* __restrict__ rmt,
+                                                         uint16_t* __restrict__ sh, uint16_t* __restrict__ sht) {
+  __shared__ float tile[64][65];
+  const int hb = H / 64;
+  const int r0 = (blockIdx.x / hb) * 64, c0 = (blockIdx.x % hb) * 64;
+  const int t = threadIdx.x;
+  {
+    const int rr = t >> 4, c4 = (t & 15) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rr + 16 * i;
+      const int64_t o = (int64_t)(r0 + r) * H + c0 + c4;
+      const f32x4 wi = *reinterpret_cast<const f32x4*>(w + o), gi = *reinterpret_cast<const f32x4*>(g + o);
+      f32x4 mi = *reinterpret_cast<const f32x4*>(m + o), vi = *reinterpret_cast<const f32x4*>(v + o);
+      f32x4 nw;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a = mi[e], b = vi[e];
+        nw[e] = adamw_elem(wi[e], gi[e], a, b, lr, b1, b2, b1c, b2c, eps, wd);
+        mi[e] = a;
+        vi[e] = b;
+        tile[r][c4 + e] = nw[e];
+      }
+      *reinterpret_cast<f32x4*>(m + o) = mi;
+      *reinterpret_cast<f32x4*>(v + o) = vi;
+      *reinterpret_cast<f32x4*>(w + o) = nw;
+      u32x2 q;
+      q.x = pack_bf16x2(nw[0], nw[1]);
+      q.y = pack_bf16x2(nw[2], nw[3]);
+      *reinterpret_cast<u32x2*>(rm + o) = q;
+    }
+  }
+  __syncthreads();
+  {
+    // [H,S] row-major: column c of the tile, 16 consecutive rows per thread
+    const int c = t >> 2, rs = (t & 3) * 16;
+    uint16_t* dst = rmt + (int64_t)(c0 + c) * S + r0 + rs;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 q;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        q[e] = pack_bf16x2(tile[rs + 8 * h + 2 * e][c], tile[rs + 8 * h + 2 * e + 1][c]);
+      *reinterpret_cast<u32x4*>(dst + 8 * h) = q;
+    }
+  }
+  {
+    // fragment layout: (substep s, lane) chunk t of a 32 x 64 block holds
+    // row (lane & 31), K = 16 s + 8 (lane >> 5) .. +7
+    const int s = t >> 6, lane = t & 63;
+    const int rr = lane & 31, kq = 16 * s + 8 * (lane >> 5);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int br = half * 32 + rr;
+      u32x4 q, qt;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        q[e] = pack_bf16x2(tile[br][kq + 2 * e], tile[br][kq + 2 * e + 1]);     // B = W [S rows, K = H]
+        qt[e] = pack_bf16x2(tile[kq + 2 * e][br], tile[kq + 2 * e + 1][br]);    // B = W^T [H rows, K = S]
+      }
+      const int64_t blk = (int64_t)(r0 / 32 + half) * hb + c0 / 64;
+      const int64_t blkt = (int64_t)(c0 / 32 + half) * (S / 64) + r0 / 64;
+      *reinterpret_cast<u32x4*>(sh + blk * kShufBlock + t * 8) = q;
+      *reinterpret_cast<u32x4*>(sht + blkt * kShufBlock + t * 8) = qt;
+    }
+  }
+}
+
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 static int grid_n(int64_t n) {
   int64_t b = cdiv(n, 256);
@@ -120,6 +205,20 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
     for (int p = 0; p < 3; ++p) {
       if (!masters[p] || !(proj_mask & (1 << p))) continue;
       float* w = const_cast<float*>(masters[p]);
+      float* gp = grads[j] + p * sh;
+      float* mp = m[j] + p * sh;
+      float* vp = v[j] + p * sh;
+      uint16_t* pk = packed_out ? packed_out[j] : nullptr;
+      if (pk && sl.s % 64 == 0 && sl.h % 64 == 0 && al16(w) && al16(gp) && al16(mp) && al16(vp)) {
+        const int64_t tiles = sh / 4096;
+        GLT_CHECK(tiles < (1ll << 31), GLT_ERR_SHAPE, "glt_adamw_graft_step: %lld tiles", (long long)tiles);
+        uint16_t* rm = pk + 2 * p * sh;
+        GLT_LAUNCH("adamw_pack", adamw_pack_kernel, dim3((unsigned)tiles), dim3(256), 0, st, w, gp, mp, vp,
+                   sl.s, sl.h, lr, beta1, beta2, b1c, b2c, eps, weight_decay, rm, rm + sh,
+                   pk + packed_shuf_offset(sl.s, sl.h, 2 * p), pk + packed_shuf_offset(sl.s, sl.h, 2 * p + 1));
+        GLT_LAUNCH_CHECK("adamw_pack");
+        continue;
+      }
       GLT_LAUNCH("adamw", adamw_kernel, dim3(grid_n(sh)), dim3(256), 0, st, w, grads[j] + p * sh,
                          m[j] + p * sh, v[j] + p * sh, (uint16_t*)nullptr, sh, lr, beta1, beta2, b1c, b2c, eps,
                          weight_decay, (const float*)nullptr, 0, 0.f);

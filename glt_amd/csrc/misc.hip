@@ -112,10 +112,50 @@ __global__ void __launch_bounds__(256) transpose_kernel(const Tin* __restrict__ 
   }
 }
 
+// bf16 transpose of whole 64 x 64 tiles with 16-byte accesses on both
+// sides: rows arrive as 8-element chunks into an LDS tile (row pitch 72
+// elements keeps the chunks 16-byte aligned), then lane l of each wavefront
+// gathers eight consecutive rows of tile column l (adjacent lanes read
+// adjacent halves of one LDS word) and writes them as one 16-byte chunk of
+// output row c0 + l.
+__global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* __restrict__ src,
+                                                          uint16_t* __restrict__ dst, int rows, int cols,
+                                                          int64_t src_ld) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][72];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = t + 256 * i, r = q >> 3, k = (q & 7) * 8;
+    *reinterpret_cast<u32x4*>(&tile[r][k]) =
+        *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + r) * src_ld + c0 + k);
+  }
+  __syncthreads();
+  const int w = t >> 6, l = t & 63;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int j = 2 * w + i;
+    u32x4 q;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      q[e] = (uint32_t)tile[8 * j + 2 * e][l] | ((uint32_t)tile[8 * j + 2 * e + 1][l] << 16);
+    *reinterpret_cast<u32x4*>(dst + (int64_t)(c0 + l) * rows + r0 + 8 * j) = q;
+  }
+}
+
 template <typename Tin, typename Tout>
 static glt_status launch_transpose(const Tin* src, Tout* dst, int rows, int cols, int64_t src_ld,
                                    hipStream_t st) {
   if (rows == 0 || cols == 0) return GLT_OK;
+  if constexpr (sizeof(Tin) == 2 && sizeof(Tout) == 2) {
+    const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    if (al && rows % 64 == 0 && cols % 64 == 0 && src_ld % 8 == 0) {
+      dim3 grid((unsigned)(cols / 64), (unsigned)(rows / 64));
+      GLT_LAUNCH("transpose16", transpose16_kernel, grid, dim3(256), 0, st, src, dst, rows, cols, src_ld);
+      GLT_LAUNCH_CHECK("transpose16");
+      return GLT_OK;
+    }
+  }
   dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64));
   GLT_LAUNCH("transpose", (transpose_kernel<Tin, Tout>), grid, dim3(256), 0, st, src, dst, rows, cols, src_ld);
   GLT_LAUNCH_CHECK("transpose");

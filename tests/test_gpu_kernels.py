@@ -220,24 +220,30 @@ def test_adamw(dev, clip):
     np.testing.assert_array_equal(_bits(mir), O.f32_to_bf16_bits(to_np(wd_)))
 
 
-def test_adamw_graft_step_refreshes_packed_mirror(dev):
+@pytest.mark.parametrize("S,H", [(64, 96), (128, 192)])   # H % 64 != 0: separate passes; else the fused kernel
+def test_adamw_graft_step_refreshes_packed_mirror(dev, S, H):
     import torch
     from glt_amd import ops
-    S, H = 64, 96
     ms = [torch.from_numpy(draw((S, H), 9, p, 0, 0.02, bf16=False)).cuda() for p in range(3)]
     sl = ops.GraftSlice(0, S, 0, H, *ms).pack()
-    grads = torch.from_numpy(draw((3 * S * H,), 10, 1, 0, 0.01, bf16=False)).cuda()
     m = torch.zeros(3 * S * H, device=dev)
     v = torch.zeros(3 * S * H, device=dev)
-    w0 = [to_np(t).copy() for t in ms]
-    ops.adamw_graft_step([sl], [grads], [m], [v], 0, 1e-4)
-    torch.cuda.synchronize()
-    gn = to_np(grads).reshape(3, S, H)
+    w = [to_np(t).copy() for t in ms]
+    rm = [np.zeros((S, H), np.float32) for _ in range(3)]
+    rv = [np.zeros((S, H), np.float32) for _ in range(3)]
+    for step in range(2):
+        grads = torch.from_numpy(draw((3 * S * H,), 10 + step, 1, 0, 0.01, bf16=False)).cuda()
+        ops.adamw_graft_step([sl], [grads], [m], [v], step, 1e-4)
+        torch.cuda.synchronize()
+        gn = to_np(grads).reshape(3, S, H)
+        for p in range(3):
+            w[p], rm[p], rv[p] = O.adamw(w[p], gn[p], rm[p], rv[p], step, 1e-4, 0.9, 0.999, 1e-8, 0.01)
     rowmajor, shuf = packed_views(O.bf16_bits_to_f32(_bits(sl.packed)), S, H)
+    mn, vn = to_np(m).reshape(3, S, H), to_np(v).reshape(3, S, H)
     for p in range(3):
-        rw, _, _ = O.adamw(w0[p], gn[p], np.zeros((S, H), np.float32), np.zeros((S, H), np.float32), 0, 1e-4,
-                           0.9, 0.999, 1e-8, 0.01)
-        assert_f32_close(to_np(ms[p]), rw, tol=1e-6)
+        assert_f32_close(to_np(ms[p]), w[p], tol=1e-6)
+        assert_f32_close(mn[p], rm[p], tol=1e-5, what="m")
+        assert_f32_close(vn[p], rv[p], tol=1e-5, what="v")
         wb = O.bf16_round(to_np(ms[p]))
         np.testing.assert_array_equal(rowmajor[2 * p], wb)
         np.testing.assert_array_equal(rowmajor[2 * p + 1], wb.T)
@@ -284,6 +290,22 @@ def test_silu_mul_and_gate_up_bwd(dev):
     rdg, rdu = O.gate_up_bwd(gi, g, u)
     assert_f32_close(to_np(dg), rdg, tol=1e-5)
     assert_f32_close(to_np(du), rdu, tol=1e-5)
+
+
+@pytest.mark.parametrize("rows,cols,dt", [(128, 192, "bf16"), (16384 // 8, 1024, "bf16"), (100, 72, "bf16"),
+                                         (64, 64, "f32"), (33, 65, "f32")])
+def test_transpose_exact(dev, rows, cols, dt):
+    """glt_transpose: whole 64x64 bf16 tiles take the 16-byte path, other
+    shapes and f32 the element path; either way a bit-exact transpose."""
+    import torch
+    from glt_amd import _ffi as F
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    x = torch.randn(rows, cols, device=dev).to(tdt)
+    y = torch.full((cols, rows), 7.0, device=dev).to(tdt)
+    F.call("glt_transpose", x.data_ptr(), y.data_ptr(), rows, cols, F.DTYPE_BF16 if dt == "bf16" else F.DTYPE_F32,
+           None)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), x.cpu().t().contiguous())
 
 
 def test_f32_to_bf16_bitexact(dev):
