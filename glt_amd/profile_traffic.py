@@ -26,7 +26,7 @@ KERNELS = {
     "wgrad": ("gemm_mfma_kernel<float, 0, false>", lambda g: g < 256 * 256),
     "rmsnorm_fwd": ("rmsnorm_fwd", None),
     "rmsnorm_bwd": ("rmsnorm_bwd", None),
-    "adamw": ("adamw_kernel", None),
+    "adamw_pack": ("adamw_pack_kernel", None),
     "rope": ("rope_kernel", None),
     "bake": ("bake_kernel", None),
 }
