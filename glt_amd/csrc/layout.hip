@@ -70,6 +70,55 @@ __global__ void __launch_bounds__(256) shuffle_kernel(const TS* __restrict__ src
   *reinterpret_cast<u32x4*>(dst + (int64_t)blk * kShufBlock + t * 8) = q;
 }
 
+// Transposed bf16 source (B[n][k] = src[k][n]) in whole 64 x 64 tiles, one
+// tile per wavefront: the tile is the two 32-row fragment blocks (n0/32,
+// n0/32 + 1) of K block k0/64. Lane (cb = lane & 7, kb = lane >> 3) loads
+// the 8 x 8 sub-block at source rows k0 + 8 kb .. +7, columns n0 + 8 cb ..
+// +7 (each load instruction covers eight whole 128-byte lines) and
+// transposes it in registers: column c becomes the 16-byte chunk of B row
+// n0 + 8 cb + c holding K = k0 + 8 kb .. +7, which is chunk (substep kb/2,
+// lane (8 cb + c) % 32 + 32 (kb & 1)) of its block. The chunks go to their
+// place in the wavefront's 8 KB of LDS and leave as contiguous 1 KB stores.
+__global__ void __launch_bounds__(256) shuffle_tr16_kernel(const uint16_t* __restrict__ src, int64_t ld, int rows,
+                                                           int K, uint16_t* __restrict__ dst) {
+  __shared__ __attribute__((aligned(16))) uint16_t stage[4][2 * kShufBlock];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  const int kt = K / 64;
+  if (tile >= (int64_t)(rows / 64) * kt) return;
+  const int nt = (int)(tile / kt), ktile = (int)(tile % kt);
+  const int n0 = nt * 64, k0 = ktile * 64;
+  const int cb = lane & 7, kb = lane >> 3;
+  u32x4 in[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    in[r] = *reinterpret_cast<const u32x4*>(src + (int64_t)(k0 + 8 * kb + r) * ld + n0 + 8 * cb);
+  uint16_t* st = stage[wave];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = __builtin_amdgcn_perm(in[2 * w + 1][c >> 1], in[2 * w][c >> 1], sel);
+    const int n = 8 * cb + c;
+    const int chunk = (kb >> 1) * 64 + (n & 31) + 32 * (kb & 1);
+    *reinterpret_cast<u32x4*>(st + (n >> 5) * kShufBlock + chunk * 8) = o;
+  }
+  // the wavefront's LDS accesses execute in order; the fences keep the
+  // compiler from moving the reads above the writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint16_t* out = dst + ((int64_t)(2 * nt + h) * kt + ktile) * kShufBlock;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4*>(out + (i * 64 + lane) * 8) =
+          *reinterpret_cast<const u32x4*>(st + h * kShufBlock + (i * 64 + lane) * 8);
+  }
+}
+
 glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed, int rows, int K, uint16_t* dst,
                      hipStream_t st) {
   GLT_CHECK(rows >= 0 && K >= 0, GLT_ERR_SHAPE, "shuffle_b: negative shape");
@@ -85,6 +134,14 @@ glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed
     else GLT_LAUNCH("shuffle", (shuffle_kernel<float, false>), grid, dim3(256), 0, st, s, ld, rows, K, kblocks, dst);
   } else {
     const uint16_t* s = static_cast<const uint16_t*>(src);
+    if (transposed && rows % 64 == 0 && K % 64 == 0 && ld % 8 == 0 &&
+        ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
+      const int64_t tiles = (int64_t)(rows / 64) * (K / 64);
+      GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, s, ld, rows, K,
+                 dst);
+      GLT_LAUNCH_CHECK("shuffle_tr");
+      return GLT_OK;
+    }
     if (transposed) GLT_LAUNCH("shuffle", (shuffle_kernel<uint16_t, true>), grid, dim3(256), 0, st, s, ld, rows, K, kblocks, dst);
     else GLT_LAUNCH("shuffle", (shuffle_kernel<uint16_t, false>), grid, dim3(256), 0, st, s, ld, rows, K, kblocks, dst);
   }

@@ -112,34 +112,34 @@ __global__ void __launch_bounds__(256) transpose_kernel(const Tin* __restrict__ 
   }
 }
 
-// bf16 transpose of whole 64 x 64 tiles with 16-byte accesses on both
-// sides: rows arrive as 8-element chunks into an LDS tile (row pitch 72
-// elements keeps the chunks 16-byte aligned), then lane l of each wavefront
-// gathers eight consecutive rows of tile column l (adjacent lanes read
-// adjacent halves of one LDS word) and writes them as one 16-byte chunk of
-// output row c0 + l.
+// bf16 transpose of whole 64 x 64 tiles, one tile per wavefront, no LDS.
+// Lane (cb = lane & 7, kb = lane >> 3) owns the 8 x 8 sub-block at source
+// rows 8 kb .. +7 and columns 8 cb .. +7: it loads the eight 16-byte row
+// pieces (each load instruction covers eight whole 128-byte lines),
+// transposes the block in registers with byte permutes, and stores eight
+// 16-byte pieces of output rows 8 cb .. +7 (again eight whole lines per
+// instruction).
 __global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* __restrict__ src,
                                                           uint16_t* __restrict__ dst, int rows, int cols,
                                                           int64_t src_ld) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[64][72];
-  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-  const int t = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tcols = cols / 64;
+  if (tile >= (int64_t)(rows / 64) * tcols) return;
+  const int r0 = (int)(tile / tcols) * 64, c0 = (int)(tile % tcols) * 64;
+  const int cb = lane & 7, kb = lane >> 3;
+  u32x4 in[8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = t + 256 * i, r = q >> 3, k = (q & 7) * 8;
-    *reinterpret_cast<u32x4*>(&tile[r][k]) =
-        *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + r) * src_ld + c0 + k);
-  }
-  __syncthreads();
-  const int w = t >> 6, l = t & 63;
+  for (int r = 0; r < 8; ++r)
+    in[r] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + 8 * kb + r) * src_ld + c0 + 8 * cb);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int j = 2 * w + i;
-    u32x4 q;
+  for (int c = 0; c < 8; ++c) {
+    // output word w of column c = (row 2w, row 2w+1) halves c & 1 of word c / 2
+    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      q[e] = (uint32_t)tile[8 * j + 2 * e][l] | ((uint32_t)tile[8 * j + 2 * e + 1][l] << 16);
-    *reinterpret_cast<u32x4*>(dst + (int64_t)(c0 + l) * rows + r0 + 8 * j) = q;
+    for (int w = 0; w < 4; ++w) o[w] = __builtin_amdgcn_perm(in[2 * w + 1][c >> 1], in[2 * w][c >> 1], sel);
+    *reinterpret_cast<u32x4*>(dst + (int64_t)(c0 + 8 * cb + c) * rows + r0 + 8 * kb) = o;
   }
 }
 
@@ -150,8 +150,10 @@ static glt_status launch_transpose(const Tin* src, Tout* dst, int rows, int cols
   if constexpr (sizeof(Tin) == 2 && sizeof(Tout) == 2) {
     const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
     if (al && rows % 64 == 0 && cols % 64 == 0 && src_ld % 8 == 0) {
-      dim3 grid((unsigned)(cols / 64), (unsigned)(rows / 64));
-      GLT_LAUNCH("transpose16", transpose16_kernel, grid, dim3(256), 0, st, src, dst, rows, cols, src_ld);
+      const int64_t tiles = (int64_t)(rows / 64) * (cols / 64);
+      GLT_CHECK(tiles < (1ll << 33), GLT_ERR_SHAPE, "transpose: %lld tiles", (long long)tiles);
+      GLT_LAUNCH("transpose16", transpose16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, src, dst, rows,
+                 cols, src_ld);
       GLT_LAUNCH_CHECK("transpose16");
       return GLT_OK;
     }

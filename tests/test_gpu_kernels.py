@@ -308,6 +308,30 @@ def test_transpose_exact(dev, rows, cols, dt):
     assert torch.equal(y.cpu(), x.cpu().t().contiguous())
 
 
+@pytest.mark.parametrize("V,D", [(192, 128), (100, 96), (4096, 512)])
+def test_lm_head_prepare_fragment_layout(dev, V, D):
+    """glt_lm_head_prepare writes lm_head [V,D] and its transpose [D,V] in
+    the MFMA fragment layout, bit for bit. Whole 64 x 64 tiles of the
+    transpose go through the register-transpose path, ragged shapes through
+    the LDS tile path."""
+    import torch
+    from glt_amd import _ffi as F
+    lib = F.load()
+    w = torch.from_numpy(draw((V, D), 21, V, 0, 1.0)).to(dev).to(torch.bfloat16)
+    prep = torch.full((lib.glt_lm_head_prepared_size(V, D),), 0x55, dtype=torch.uint8, device=dev)
+    F.call("glt_lm_head_prepare", w.data_ptr(), V, D, prep.data_ptr(), None)
+    torch.cuda.synchronize()
+    wf = w.float().cpu().numpy()
+    n_fwd = (-(-V // 32) * 32) * (-(-D // 64) * 64)
+    off = -(-(n_fwd * 2) // 256) * 256
+    n_t = (-(-D // 32) * 32) * (-(-V // 64) * 64)
+    got = prep.cpu().numpy()
+    fwd = got[:n_fwd * 2].view(np.uint16)
+    tr = got[off:off + n_t * 2].view(np.uint16)
+    np.testing.assert_array_equal(fwd, O.f32_to_bf16_bits(shuffle_b(wf)))
+    np.testing.assert_array_equal(tr, O.f32_to_bf16_bits(shuffle_b(wf.T)))
+
+
 def test_f32_to_bf16_bitexact(dev):
     import torch
     from glt_amd import ops
