@@ -38,7 +38,7 @@ typedef int32_t glt_status;
 #define GLT_ERR_ALREADY_BAKED      6  /* second bake on the same model state       */
 #define GLT_ERR_BAKED_NO_BACKWARD  7  /* backward on a shadow-baked model          */
 #define GLT_ERR_HIP                8  /* a HIP runtime call failed                 */
-#define GLT_ERR_UNSUPPORTED        9  /* valid request this build does not serve   */
+#define GLT_ERR_UNSUPPORTED        9  /* valid request the library does not serve  */
 #define GLT_ERR_IO                10  /* a file could not be opened, read or written */
 #define GLT_ERR_FORMAT            11  /* file content malformed or not the expected  */
 #define GLT_ERR_NOT_FOUND         12  /* a named tensor is absent from the files     */

@@ -1,7 +1,7 @@
 /*
  * glt_oracle.c — CPU restatement of the reference's grafted-SwiGLU layer path.
  *
- * TEST INFRASTRUCTURE ONLY. This file is the checker the GPU library is
+ * TEST INFRASTRUCTURE ONLY. This file is the oracle the GPU library is
  * compared against; it is loaded by tests/, by __graft_entry__.smoke() and by
  * bench.py's cpu_baseline leg, and by nothing on the product path.
  *

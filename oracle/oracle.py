@@ -1,7 +1,7 @@
 """numpy/ctypes front end of the C oracle (glt_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg as the checker; never by the glt_amd package.
+bench.py's cpu_baseline leg; never by the glt_amd package.
 
 All arrays are numpy float32 holding bf16-representable values where the
 reference holds bf16 (use bf16_round to get there). Citations of the
@@ -379,7 +379,7 @@ def fnv1a64(data, h=FNV_BASIS):
 
 
 def eval_stats(logits, ids):
-    """Shadow-eval terms (reference grafting.hip:504-547) in this build's
+    """Shadow-eval terms (reference grafting.hip:504-547) in the library's
     row-parallel hash form: each row's f32 logits hashed with FNV-1a, the
     row hashes' little-endian bytes chained in row order; f64 NLL of rows
     t < T-1 against ids[b, t+1]; f64 sum and sum of squares."""
