@@ -636,28 +636,38 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
         const __amdgpu_buffer_rsrc_t r1 = uni_rsrc(P.out1, kExtent);
         const __amdgpu_buffer_rsrc_t rG = uni_rsrc(P.aux0, kExtent);
         const __amdgpu_buffer_rsrc_t rU = uni_rsrc(P.aux1, kExtent);
+        // Halves h = 2 i + jh; the loop over the four row blocks i stays
+        // rolled (only the accumulator block of a half needs a constant
+        // index, chosen by a switch), which keeps this epilogue's code a
+        // quarter of its unrolled size.
         u32x2 ga[2][8], ua[2][8];
-        auto aux = [&](int h) {
-          const int i = h >> 1, jh = h & 1;
+        auto aux = [&](int i, int jh, int slot) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
             const uint32_t o = ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldaux, 2);
-            ga[h & 1][k] = __builtin_amdgcn_raw_buffer_load_b64(rG, o, 0, 0);
-            ua[h & 1][k] = __builtin_amdgcn_raw_buffer_load_b64(rU, o, 0, 0);
+            ga[slot][k] = __builtin_amdgcn_raw_buffer_load_b64(rG, o, 0, 0);
+            ua[slot][k] = __builtin_amdgcn_raw_buffer_load_b64(rU, o, 0, 0);
           }
         };
-        aux(0);
+        aux(0, 0, 0);
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int h = 0; h < 8; ++h) {
-          const int i = h >> 1, jh = h & 1;
-          if (h + 1 < 8) aux(h + 1);
-          stage(i, jh, 1.0f);
+        for (int jh = 0; jh < 2; ++jh) {
+          if (jh == 0) aux(i, 1, 1);
+          else if (i < 3) aux(i + 1, 0, 0);
+          switch (i) {
+            case 0: stage(0, jh, 1.0f); break;
+            case 1: stage(1, jh, 1.0f); break;
+            case 2: stage(2, jh, 1.0f); break;
+            default: stage(3, jh, 1.0f); break;
+          }
           wave_lds_sync();
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
             const f32x4 a4 = fetch(k);
             const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-            const u32x2 gk = ga[h & 1][k], uk = ua[h & 1][k];
+            const u32x2 gk = ga[jh][k], uk = ua[jh][k];
             const float gv[4] = {__uint_as_float(gk.x << 16), __uint_as_float(gk.x & 0xFFFF0000u),
                                  __uint_as_float(gk.y << 16), __uint_as_float(gk.y & 0xFFFF0000u)};
             const float uv[4] = {__uint_as_float(uk.x << 16), __uint_as_float(uk.x & 0xFFFF0000u),
@@ -675,6 +685,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
             __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2_hw(du[0], du[1]), pack2_hw(du[2], du[3])}, r1, o, 0, 0);
           }
           wave_lds_sync();
+        }
         }
       }
     }
