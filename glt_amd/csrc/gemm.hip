@@ -139,6 +139,9 @@ constexpr int kBM = 256, kBK = 64;
 constexpr int kTileElems = kBM * kBK;                    // one A tile = one LDS stage (32 KB)
 constexpr int kAStages = 4;
 constexpr uint32_t kExtent = 0x7FFFFFF0u;                // buffer extent below kOob
+// cache policy of the epilogue's streams (written or read once here, used
+// again only by another kernel): the nontemporal bit
+constexpr int kNt = 2;
 constexpr int kEpWaveBytes = 8192;                         // epilogue staging per wavefront
 constexpr size_t kMfmaLds = (size_t)kAStages * kTileElems * 2 + 4 * kEpWaveBytes;  // 160 KB
 constexpr uint32_t kShufStepBytes = kShufBlock * 2;      // one 32 x 64 block of B (4 KB)
@@ -523,7 +526,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
           }
         }
 #pragma unroll
-        for (int k = 0; k < 32 / kRowsPerRead; ++k) __builtin_amdgcn_raw_buffer_store_b128(q[k], r, o[k], 0, 0);
+        for (int k = 0; k < 32 / kRowsPerRead; ++k) __builtin_amdgcn_raw_buffer_store_b128(q[k], r, o[k], 0, kNt);
       };
       if constexpr (MODE == EPI_STORE || MODE == EPI_RESID) {
         const float alpha = P.alpha;
@@ -645,8 +648,8 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
             const uint32_t o = ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldaux, 2);
-            ga[slot][k] = __builtin_amdgcn_raw_buffer_load_b64(rG, o, 0, 0);
-            ua[slot][k] = __builtin_amdgcn_raw_buffer_load_b64(rU, o, 0, 0);
+            ga[slot][k] = __builtin_amdgcn_raw_buffer_load_b64(rG, o, 0, kNt);
+            ua[slot][k] = __builtin_amdgcn_raw_buffer_load_b64(rU, o, 0, kNt);
           }
         };
         aux(0, 0, 0);
@@ -681,8 +684,8 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
               du[e] = av[e] * (gv[e] * sg);
             }
             const uint32_t o = ooff(rbase + 32 * i + 4 * k + rr0, cbase + 64 * jh + 4 * rc, P.ldo, 2);
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2_hw(dg[0], dg[1]), pack2_hw(dg[2], dg[3])}, r0, o, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2_hw(du[0], du[1]), pack2_hw(du[2], du[3])}, r1, o, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2_hw(dg[0], dg[1]), pack2_hw(dg[2], dg[3])}, r0, o, 0, kNt);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2_hw(du[0], du[1]), pack2_hw(du[2], du[3])}, r1, o, 0, kNt);
           }
           wave_lds_sync();
         }
