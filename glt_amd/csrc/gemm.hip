@@ -83,7 +83,9 @@ __device__ __forceinline__ void epilogue(const GProb& P, int m, int n, float a0,
 // Locates problem and tile of tile index t. Within a problem tiles run in
 // groups of kGroupM M-tiles, so tiles with neighbouring indices share A and
 // B rows in L2.
-constexpr int kGroupM = 8;
+// (4 measured best of 1, 2, 4, 8, 16 on the step's GEMMs: each XCD's 32
+// tiles of a round form a 4 x 8 block.)
+constexpr int kGroupM = 4;
 __device__ __forceinline__ int locate_tile(const GArgs& args, int t, int& tm, int& tn) {
   int pi = 0;
   while (pi + 1 < args.nprob && t >= args.p[pi + 1].tile_begin) ++pi;
