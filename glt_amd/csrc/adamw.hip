@@ -209,7 +209,7 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
       float* mp = m[j] + p * sh;
       float* vp = v[j] + p * sh;
       uint16_t* pk = packed_out ? packed_out[j] : nullptr;
-      if (pk && sl.s % 64 == 0 && sl.h % 64 == 0 && al16(w) && al16(gp) && al16(mp) && al16(vp)) {
+      if (pk && sl.s % 64 == 0 && sl.h % 64 == 0 && al16(w) && al16(gp) && al16(mp) && al16(vp) && al16(pk)) {
         const int64_t tiles = sh / 4096;
         GLT_CHECK(tiles < (1ll << 31), GLT_ERR_SHAPE, "glt_adamw_graft_step: %lld tiles", (long long)tiles);
         uint16_t* rm = pk + 2 * p * sh;
