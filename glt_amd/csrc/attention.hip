@@ -322,10 +322,14 @@ extern "C" glt_status glt_attention_fwd(const void* q, const void* k, const void
   // K rows are addressed through 31-bit buffer offsets
   GLT_CHECK((int64_t)B * T * Hkv * kHd * 2 < (int64_t)kOob, GLT_ERR_SHAPE, "glt_attention_fwd: K of %lld bytes",
             (long long)B * T * Hkv * kHd * 2);
-  static bool attr_set = false;
-  if (!attr_set) {
+  // the dynamic-LDS limit is a per-device attribute of the kernel
+  static bool attr_set[64] = {};
+  int dev = 0;
+  GLT_TRY_HIP(hipGetDevice(&dev));
+  GLT_CHECK(dev >= 0 && dev < 64, GLT_ERR_HIP, "glt_attention_fwd: device index %d out of range", dev);
+  if (!attr_set[dev]) {
     GLT_TRY_HIP(hipFuncSetAttribute((const void*)attn_fwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kAttnLds));
-    attr_set = true;
+    attr_set[dev] = true;
   }
   const float scale_log2 = scale * 1.4426950408889634f;
   // 1-D over (query block, batch, head)

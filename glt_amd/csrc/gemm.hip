@@ -817,12 +817,16 @@ static glt_status device_cus(int& cus) {
 
 template <typename TO, int MODE, bool DUAL>
 static glt_status launch_mfma(const GArgs& a, hipStream_t st, const char* label) {
-  static bool attr_set = false;
+  // the dynamic-LDS limit is a per-device attribute of the kernel
+  static bool attr_set[64] = {};
   auto fn = gemm_mfma_kernel<TO, MODE, DUAL>;
-  if (!attr_set) {
+  int dev = 0;
+  GLT_TRY_HIP(hipGetDevice(&dev));
+  GLT_CHECK(dev >= 0 && dev < 64, GLT_ERR_HIP, "gemm: device index %d out of range", dev);
+  if (!attr_set[dev]) {
     GLT_TRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLds));
-    attr_set = true;
+    attr_set[dev] = true;
   }
   int cus = 0;
   const glt_status rc = device_cus(cus);
