@@ -47,3 +47,33 @@ def test_attention_uniform_queries_give_prefix_means(dev):
         g = h // (Hq // Hkv)
         prefix = np.cumsum(v[0, :, g].astype(np.float64), axis=0) / np.arange(1, T + 1)[:, None]
         assert_bf16_budget(out[0, :, h], prefix, q=3, what=f"head {h}")
+
+
+def test_attention_full_decoder_layer_shape(dev):
+    """The decoder layer's attention at its full size (2 x 4096 tokens, 32
+    query / 8 kv heads of 128, causal): sampled query rows of every head
+    against float64 softmax(q k^T / sqrt(128)) v over the row's causal
+    prefix; the sample spans query blocks and key tiles and the last token."""
+    import torch
+    from glt_amd import ops
+    B, T, Hq, Hkv, hd = 2, 4096, 32, 8, 128
+    bf = torch.bfloat16
+    q = ops.fill_normal(torch.empty((B, T, Hq, hd), dtype=bf, device="cuda"), 31, 1, 0.0, 1.0)
+    k = ops.fill_normal(torch.empty((B, T, Hkv, hd), dtype=bf, device="cuda"), 31, 2, 0.0, 1.0)
+    v = ops.fill_normal(torch.empty((B, T, Hkv, hd), dtype=bf, device="cuda"), 31, 3, 0.0, 1.0)
+    out = ops.attention(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    kn, vn = to_np(k).astype(np.float64), to_np(v).astype(np.float64)
+    rows = [0, 63, 64, 127, 128, 1000, 2047, 4095]
+    qn = to_np(q[:, rows]).astype(np.float64)                       # [B, rows, Hq, hd]
+    got = to_np(out[:, rows])
+    ref = np.empty_like(got, dtype=np.float64)
+    rep = Hq // Hkv
+    for b in range(B):
+        for i, t in enumerate(rows):
+            for h in range(Hq):
+                g = h // rep
+                s = kn[b, :t + 1, g] @ qn[b, i, h] / np.sqrt(hd)
+                p = np.exp(s - s.max())
+                ref[b, i, h] = (p / p.sum()) @ vn[b, :t + 1, g]
+    assert_bf16_budget(got, ref, q=3, what="attention at the decoder-layer shape")
