@@ -108,3 +108,42 @@ def test_silence_kernels_match_oracle(tokens, sl):
     assert np.allclose(dyg.cpu().numpy(), rg, rtol=1e-5, atol=1e-6)
     assert np.allclose(dyu.cpu().numpy(), ru, rtol=1e-5, atol=1e-6)
     assert np.allclose(eg.cpu().numpy(), reg, rtol=1e-5) and np.allclose(eu.cpu().numpy(), reu, rtol=1e-5)
+
+
+def test_masked_ce_full_size_properties():
+    """The benchmarked size (4 x 4096 positions, Llama-3 vocabulary 128256):
+    n counts the unmasked shifted positions exactly; the loss is the mean
+    of the per-token CE over them; sampled rows' CE and gradient match the
+    oracle (each row posed as its own two-position sequence, the gradient
+    rescaled from the sample's n to the full n); masked rows and the last
+    position of each sequence carry no gradient."""
+    import torch
+    from glt_amd import ops
+    B, T, V = 4, 4096, 128256
+    logits = ops.fill_normal(torch.empty((B, T, V), dtype=torch.bfloat16, device="cuda"), 41, 1, 0.0, 3.0)
+    gen = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, V, (B, T), generator=gen, dtype=torch.int32)
+    ood = (torch.rand((B, T), generator=gen) < 0.25).to(torch.int32)
+    stats, g, ce = ops.masked_ce(logits, ids.cuda(), ood.cuda(), 1.0, ce_per_token=True)
+    torch.cuda.synchronize()
+    st = stats.cpu().numpy()
+    valid = (1 - ood[:, 1:]).reshape(-1).numpy().astype(bool)
+    n = int(valid.sum())
+    assert st[3] == n
+    cen = ce.cpu().numpy()[:B * (T - 1)].astype(np.float64)
+    assert st[0] == pytest.approx(cen[valid].sum() / n, rel=1e-4)
+    samples = [(0, 0), (0, 1), (1, 2047), (2, 4000), (3, 4094), (3, 17)]
+    sv = [(b, t) for b, t in samples if not ood[b, t + 1]]
+    sm = [(b, t) for b, t in samples if ood[b, t + 1]]
+    assert sv, "the sample needs unmasked rows"
+    x = np.stack([[logits[b, t].float().cpu().numpy(), np.zeros(V, np.float32)] for b, t in sv])
+    sid = np.array([[0, ids[b, t + 1]] for b, t in sv], np.int32)
+    rg, rce, rst = O.masked_ce(x, sid, None, 1.0)
+    for i, (b, t) in enumerate(sv):
+        assert abs(cen[b * (T - 1) + t] - rce[i]) <= abs(rce[i]) * 2.0 ** -7 + 1e-30
+        got = g[b, t].float().cpu().numpy()
+        ref = rg[i, 0] * (rst[3] / n)
+        assert np.abs(got - ref).max() <= np.abs(ref).max() * 2.0 ** -6, (b, t)
+    for b, t in sm:
+        assert torch.count_nonzero(g[b, t]).item() == 0
+    assert torch.count_nonzero(g[:, T - 1]).item() == 0
