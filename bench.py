@@ -201,6 +201,7 @@ def main():
                       "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
     hbm["rope"] = bench_rope(torch, F, sp, p)
     hbm["masked_ce"] = bench_masked_ce(torch, F, sp, p)
+    hbm["eval_stats"] = bench_eval_stats(torch, F, sp, p)
     hbm["torch_copy"] = bench_copy(torch)
     attention = bench_attention(torch, F, sp, p)
     layer = None
@@ -269,6 +270,38 @@ def bench_rope(torch, F, sp, p, reps=20):
     nbytes = 2 * 2 * ROPE_B * ROPE_T * (ROPE_HQ + ROPE_HK) * ROPE_HD
     return {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+
+def bench_eval_stats(torch, F, sp, p, reps=3):
+    """Shadow-eval statistics (CE sum and count, logit sum and sum of
+    squares, chained per-row FNV-1a hashes) over 4 x 4096 rows of the
+    Llama-3 vocabulary, bf16 logits; algorithmic bytes: logits read once.
+    Each row's hash chains every byte of the row, so a row is one thread's
+    sequential walk."""
+    B, T, V = CE_B, CE_T, CE_V
+    logits = torch.empty((B, T, V), dtype=torch.bfloat16, device="cuda")
+    F.call("glt_fill_normal", p(logits), F.DTYPE_BF16, logits.numel(), 501, 0, 0.0, 3.0, sp)
+    ids = torch.randint(0, V, (B, T), dtype=torch.int32, device="cuda")
+    nbytes_ws = F.load().glt_eval_stats_workspace_size(B, T)
+    ws = torch.empty(nbytes_ws, dtype=torch.uint8, device="cuda")
+    res = F.EvalResult()
+
+    def run():
+        F.call("glt_eval_stats", p(logits), V, p(ids), B, T, V, ctypes.byref(res), p(ws), nbytes_ws, sp)
+
+    run()
+    torch.cuda.synchronize()
+    F.call("glt_profile_enable", 1)
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    tot, cnt = F.profile_collect().get("eval_rows", (0.0, 1))
+    F.call("glt_profile_enable", 0)
+    t = tot / cnt
+    nbytes = 2 * B * T * V
+    del logits
+    return {"bytes": nbytes, "ms": round(t, 4), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "rows": B * T, "vocab": V}
 
 
 def bench_masked_ce(torch, F, sp, p, reps=5):

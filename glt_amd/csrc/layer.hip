@@ -246,34 +246,101 @@ struct EvalRow {
 constexpr uint64_t kFnvBasis = 1469598103934665603ULL;
 constexpr uint64_t kFnvPrime = 1099511628211ULL;
 
-__global__ void __launch_bounds__(64) eval_rows_kernel(const uint16_t* logits, int64_t ld, const int32_t* ids, int B,
-                                                       int T, int V, EvalRow* rows) {
-  const int64_t r = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  if (r >= (int64_t)B * T) return;
-  const int b = (int)(r / T), t = (int)(r - (int64_t)b * T);
-  const uint16_t* x = logits + r * ld;
-  double s = 0.0, s2 = 0.0;
-  uint64_t h = kFnvBasis;
-  float mx = -INFINITY;
-  for (int v = 0; v < V; ++v) {
-    const uint32_t bits = (uint32_t)x[v] << 16;
-    const float f = __uint_as_float(bits);
-    s += f;
-    s2 += (double)f * f;
-    mx = fmaxf(mx, f);
+// One workgroup per 16 rows, 16 threads per row: thread c of a row takes
+// chunk c of kEvalChunks chunks of ceil(V / kEvalChunks) logits (the last
+// ones shorter or empty) and accumulates its f64 sum and sum of squares,
+// its maximum and the FNV-1a hash of the chunk's f32 bytes (from the
+// basis). The row's threads then share their maxima through LDS, sum
+// exp(x - max) over their chunks, and thread 0 of the row adds the parts in
+// chunk order and hashes the chunk hashes' little-endian bytes in order.
+constexpr int kEvalChunks = 16;
+
+__device__ __forceinline__ void eval_elem(uint32_t h16, double& s, double& s2, float& mx, uint64_t& h) {
+  const uint32_t bits = h16 << 16;
+  const float f = __uint_as_float(bits);
+  s += f;
+  s2 += (double)f * f;
+  mx = fmaxf(mx, f);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      h ^= (bits >> (8 * k)) & 0xFFu;
-      h *= kFnvPrime;
+  for (int k = 0; k < 4; ++k) {
+    h ^= (bits >> (8 * k)) & 0xFFu;
+    h *= kFnvPrime;
+  }
+}
+
+__global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, int64_t ld, const int32_t* ids, int B,
+                                                        int T, int V, EvalRow* rows) {
+  __shared__ float s_max[16][kEvalChunks], s_se[16][kEvalChunks];
+  __shared__ double s_sum[16][kEvalChunks], s_sq[16][kEvalChunks];
+  __shared__ uint64_t s_h[16][kEvalChunks];
+  const int lr = threadIdx.x >> 4, c = threadIdx.x & (kEvalChunks - 1);
+  const int64_t r = (int64_t)blockIdx.x * 16 + lr;
+  const bool valid = r < (int64_t)B * T;
+  const int L = (V + kEvalChunks - 1) / kEvalChunks;
+  const int v0 = min(V, c * L), v1 = min(V, v0 + L);
+  const uint16_t* x = logits + (valid ? r : 0) * ld;
+  const bool vec = ((reinterpret_cast<uintptr_t>(x + v0) & 15) == 0) && ((v1 - v0) % 8 == 0);
+  double s = 0.0, s2 = 0.0;
+  float mx = -INFINITY;
+  uint64_t h = kFnvBasis;
+  if (valid) {
+    if (vec) {
+      for (int v = v0; v < v1; v += 8) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(x + v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          eval_elem(q[e] & 0xFFFFu, s, s2, mx, h);
+          eval_elem(q[e] >> 16, s, s2, mx, h);
+        }
+      }
+    } else {
+      for (int v = v0; v < v1; ++v) eval_elem(x[v], s, s2, mx, h);
     }
   }
-  EvalRow o{s, s2, h, 0.f, 0};
-  if (t < T - 1) {
+  s_max[lr][c] = mx;
+  __syncthreads();
+  float rmx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kEvalChunks; ++k) rmx = fmaxf(rmx, s_max[lr][k]);
+  const int b = valid ? (int)(r / T) : 0, t = valid ? (int)(r - (int64_t)b * T) : 0;
+  const bool scored = valid && t < T - 1;
+  float se = 0.f;
+  if (scored) {
+    if (vec) {
+      for (int v = v0; v < v1; v += 8) {
+        const u32x4 q = *reinterpret_cast<const u32x4*>(x + v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          se += expf(__uint_as_float(q[e] << 16) - rmx);
+          se += expf(__uint_as_float(q[e] & 0xFFFF0000u) - rmx);
+        }
+      }
+    } else {
+      for (int v = v0; v < v1; ++v) se += expf(__uint_as_float((uint32_t)x[v] << 16) - rmx);
+    }
+  }
+  s_se[lr][c] = se;
+  s_sum[lr][c] = s;
+  s_sq[lr][c] = s2;
+  s_h[lr][c] = h;
+  __syncthreads();
+  if (!valid || c != 0) return;
+  EvalRow o{0.0, 0.0, kFnvBasis, 0.f, 0};
+  float tse = 0.f;
+  for (int k = 0; k < kEvalChunks; ++k) {
+    o.sum += s_sum[lr][k];
+    o.sumsq += s_sq[lr][k];
+    tse += s_se[lr][k];
+    const uint64_t hk = s_h[lr][k];
+    for (int j = 0; j < 8; ++j) {
+      o.hash ^= (hk >> (8 * j)) & 0xFFu;
+      o.hash *= kFnvPrime;
+    }
+  }
+  if (scored) {
     const int label = ids[(int64_t)b * T + t + 1];
-    float se = 0.f;
-    for (int v = 0; v < V; ++v) se += expf(__uint_as_float((uint32_t)x[v] << 16) - mx);
     const float xl = (label >= 0 && label < V) ? __uint_as_float((uint32_t)x[label] << 16) : NAN;
-    o.nll = (mx + logf(se)) - xl;
+    o.nll = (rmx + logf(tse)) - xl;
     o.scored = 1;
   }
   rows[r] = o;
@@ -426,7 +493,7 @@ glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids
             "glt_eval_stats: needs %zu workspace bytes", glt_eval_stats_workspace_size(B, T));
   hipStream_t st = as_stream(stream);
   EvalRow* rows = static_cast<EvalRow*>(workspace);
-  GLT_LAUNCH("eval_rows", eval_rows_kernel, dim3((unsigned)((R + 63) / 64)), dim3(64), 0, st, logits, ld, ids, B, T,
+  GLT_LAUNCH("eval_rows", eval_rows_kernel, dim3((unsigned)((R + 15) / 16)), dim3(256), 0, st, logits, ld, ids, B, T,
              V, rows);
   GLT_LAUNCH_CHECK("eval_rows");
   std::vector<EvalRow> h((size_t)R);

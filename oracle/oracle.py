@@ -378,18 +378,34 @@ def fnv1a64(data, h=FNV_BASIS):
     return h
 
 
+EVAL_CHUNKS = 16
+
+
+def eval_row_hash(row):
+    """A row's hash in the library's parallel form: the row's f32 logits in
+    EVAL_CHUNKS chunks of ceil(V / EVAL_CHUNKS) elements (the last ones
+    shorter or empty), each chunk's bytes hashed with FNV-1a from the basis,
+    then the chunk hashes' little-endian bytes hashed in chunk order."""
+    b = np.asarray(row, np.float32).astype("<f4")
+    L = -(-b.size // EVAL_CHUNKS)
+    h = FNV_BASIS
+    for c in range(EVAL_CHUNKS):
+        h = fnv1a64(int(fnv1a64(b[c * L:(c + 1) * L].tobytes())).to_bytes(8, "little"), h)
+    return h
+
+
 def eval_stats(logits, ids):
     """Shadow-eval terms (reference grafting.hip:504-547) in the library's
-    row-parallel hash form: each row's f32 logits hashed with FNV-1a, the
-    row hashes' little-endian bytes chained in row order; f64 NLL of rows
-    t < T-1 against ids[b, t+1]; f64 sum and sum of squares."""
+    parallel hash form: each row hashed by eval_row_hash, the row hashes'
+    little-endian bytes chained in row order; f64 NLL of rows t < T-1
+    against ids[b, t+1]; f64 sum and sum of squares."""
     x = np.asarray(logits, np.float32)
     B, T = np.asarray(ids).shape
     V = x.shape[-1]
     rows = x.reshape(B * T, V)
     h = FNV_BASIS
     for r in rows:
-        h = fnv1a64(int(fnv1a64(r.astype("<f4").tobytes())).to_bytes(8, "little"), h)
+        h = fnv1a64(int(eval_row_hash(r)).to_bytes(8, "little"), h)
     r64 = rows.astype(np.float64)
     scored = r64.reshape(B, T, V)[:, :T - 1].reshape(-1, V)
     lab = np.asarray(ids)[:, 1:].reshape(-1)

@@ -43,9 +43,17 @@ def test_eval_hash_is_order_and_value_sensitive():
     assert O.eval_stats(y, ids)["logits_hash"] != h
     z = x[:, ::-1].copy()
     assert O.eval_stats(z, ids)["logits_hash"] != h
-    # one row: FNV-1a of the row's bytes, then of that hash's 8 bytes
+    # one row of 16: sixteen one-element chunks, each hashed from the basis,
+    # the chunk hashes' bytes hashed in order, then that row hash's 8 bytes
+    fb = lambda a: a.astype("<f4").tobytes()
     r = O.eval_stats(x[:, :1], ids[:, :1])["logits_hash"]
-    assert r == O.fnv1a64(O.fnv1a64(x[0, 0].astype("<f4").tobytes()).to_bytes(8, "little"))
+    chunks = b"".join(O.fnv1a64(fb(x[0, 0, c:c + 1])).to_bytes(8, "little") for c in range(16))
+    assert r == O.fnv1a64(O.fnv1a64(chunks).to_bytes(8, "little"))
+    # 20 elements: ten chunks of two, six empty chunks (an empty chunk hashes to the basis)
+    w = O.bf16_round(rng.normal(0, 1, 20).astype(np.float32))
+    chunks = b"".join(O.fnv1a64(fb(w[2 * c:2 * c + 2])).to_bytes(8, "little") for c in range(10))
+    chunks += O.FNV_BASIS.to_bytes(8, "little") * 6
+    assert O.eval_row_hash(w) == O.fnv1a64(chunks)
 
 
 def test_certify_gates():
