@@ -462,10 +462,12 @@ glt_status glt_model_fwd(const glt_model* m, const int32_t* ids, uint16_t* logit
  * grafting.hip:504-547): over rows (b,t) of B*T bf16 logits (row stride
  * ld), the f32 cross-entropy of rows t < T-1 against ids[b,t+1] summed in
  * f64 (total_nll; mean = total_nll / count), the f64 sum and sum of squares
- * of every logit, and a 64-bit FNV-1a hash: each row's f32 logits hashed
- * byte by byte (little-endian) from the FNV offset basis, then the row hashes'
- * 8 bytes chained in row order. (The reference chains every byte of the
- * batch in one sequence; this form is computed row-parallel, so the value
+ * of every logit, and a 64-bit FNV-1a hash: each row's f32 logits cut into
+ * 16 chunks of ceil(V/16) (the last ones shorter or empty), each chunk
+ * hashed byte by byte (little-endian) from the FNV offset basis, the chunk
+ * hashes' 8 bytes hashed in chunk order into the row hash, and the row
+ * hashes' 8 bytes chained in row order. (The reference chains every byte of
+ * the batch in one sequence; this form is computed in parallel, so the value
  * differs while serving the same purpose: equal logits give equal hashes.)
  * Synchronous; workspace: glt_eval_stats_workspace_size bytes. */
 typedef struct {
