@@ -285,7 +285,21 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
   uint64_t h = kFnvBasis;
   if (valid) {
     if (vec) {
-      for (int v = v0; v < v1; v += 8) {
+      // eight 16-byte loads in flight per thread, consumed in element order
+      int v = v0;
+      for (; v + 64 <= v1; v += 64) {
+        u32x4 q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const u32x4*>(x + v + 8 * i);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            eval_elem(q[i][e] & 0xFFFFu, s, s2, mx, h);
+            eval_elem(q[i][e] >> 16, s, s2, mx, h);
+          }
+      }
+      for (; v < v1; v += 8) {
         const u32x4 q = *reinterpret_cast<const u32x4*>(x + v);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -307,7 +321,20 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
   float se = 0.f;
   if (scored) {
     if (vec) {
-      for (int v = v0; v < v1; v += 8) {
+      int v = v0;
+      for (; v + 64 <= v1; v += 64) {
+        u32x4 q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const u32x4*>(x + v + 8 * i);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            se += expf(__uint_as_float(q[i][e] << 16) - rmx);
+            se += expf(__uint_as_float(q[i][e] & 0xFFFF0000u) - rmx);
+          }
+      }
+      for (; v < v1; v += 8) {
         const u32x4 q = *reinterpret_cast<const u32x4*>(x + v);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
