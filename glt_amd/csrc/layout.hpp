@@ -14,6 +14,18 @@
 
 namespace glt {
 
+// Transposes dst [cols, rows] = src [rows, cols] (rows src_ld elements
+// apart) of several matrices in one launch when all are bf16 in whole,
+// 16-byte-aligned 64 x 64 tiles, one launch per matrix otherwise.
+constexpr int kMaxT16Jobs = 8;
+struct T16Job {
+  const void* src;
+  void* dst;
+  int rows, cols;
+  int64_t src_ld;
+};
+glt_status transpose_batch(const T16Job* jobs, int n, int dtype, hipStream_t st);
+
 constexpr int kShufRows = 32, kShufK = 64, kShufBlock = kShufRows * kShufK;
 
 inline int64_t shuf_rows(int64_t rows) { return (rows + kShufRows - 1) / kShufRows * kShufRows; }

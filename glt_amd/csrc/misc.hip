@@ -112,20 +112,35 @@ __global__ void __launch_bounds__(256) transpose_kernel(const Tin* __restrict__ 
   }
 }
 
-// bf16 transpose of whole 64 x 64 tiles, one tile per wavefront, no LDS.
-// Lane (cb = lane & 7, kb = lane >> 3) owns the 8 x 8 sub-block at source
-// rows 8 kb .. +7 and columns 8 cb .. +7: it loads the eight 16-byte row
-// pieces (each load instruction covers eight whole 128-byte lines),
-// transposes the block in registers with byte permutes, and stores eight
-// 16-byte pieces of output rows 8 cb .. +7 (again eight whole lines per
-// instruction).
-__global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* __restrict__ src,
-                                                          uint16_t* __restrict__ dst, int rows, int cols,
-                                                          int64_t src_ld) {
+// bf16 transposes of whole 64 x 64 tiles, one tile per wavefront, no LDS,
+// several independent matrices per launch (job j owns tiles
+// [tile0[j], tile0[j+1])). Lane (cb = lane & 7, kb = lane >> 3) owns the
+// 8 x 8 sub-block at source rows 8 kb .. +7 and columns 8 cb .. +7: it
+// loads the eight 16-byte row pieces (each load instruction covers eight
+// whole 128-byte lines), transposes the block in registers with byte
+// permutes, and stores eight 16-byte pieces of output rows 8 cb .. +7
+// (again eight whole lines per instruction).
+struct T16Batch {
+  int n;
+  int64_t tile0[kMaxT16Jobs + 1];
+  const uint16_t* src[kMaxT16Jobs];
+  uint16_t* dst[kMaxT16Jobs];
+  int rows[kMaxT16Jobs], cols[kMaxT16Jobs];
+  int64_t ld[kMaxT16Jobs];
+};
+
+__global__ void __launch_bounds__(256) transpose16_kernel(const T16Batch bt) {
   const int lane = threadIdx.x & 63;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int tcols = cols / 64;
-  if (tile >= (int64_t)(rows / 64) * tcols) return;
+  int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= bt.tile0[bt.n]) return;
+  int j = 0;
+  while (j + 1 < bt.n && tile >= bt.tile0[j + 1]) ++j;
+  j = __builtin_amdgcn_readfirstlane(j);
+  tile -= bt.tile0[j];
+  const uint16_t* __restrict__ src = bt.src[j];
+  uint16_t* __restrict__ dst = bt.dst[j];
+  const int rows = bt.rows[j], tcols = bt.cols[j] / 64;
+  const int64_t src_ld = bt.ld[j];
   const int r0 = (int)(tile / tcols) * 64, c0 = (int)(tile % tcols) * 64;
   const int cb = lane & 7, kb = lane >> 3;
   u32x4 in[8];
@@ -143,19 +158,58 @@ __global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* __rest
   }
 }
 
+static bool t16_ok(const void* src, const void* dst, int rows, int cols, int64_t src_ld) {
+  const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+  return al && rows % 64 == 0 && cols % 64 == 0 && src_ld % 8 == 0;
+}
+
+glt_status transpose_any(const void* src, void* dst, int rows, int cols, int64_t src_ld, int dtype,
+                         hipStream_t st);
+
+glt_status transpose16_batch(const T16Job* jobs, int n, hipStream_t st) {
+  GLT_CHECK(n >= 0 && n <= kMaxT16Jobs, GLT_ERR_INVALID_ARG, "transpose16_batch: %d jobs", n);
+  T16Batch bt{};
+  bt.n = n;
+  int64_t tiles = 0;
+  for (int j = 0; j < n; ++j) {
+    const T16Job& J = jobs[j];
+    GLT_CHECK(t16_ok(J.src, J.dst, J.rows, J.cols, J.src_ld), GLT_ERR_SHAPE,
+              "transpose16_batch: job %d is not whole aligned 64 x 64 tiles", j);
+    bt.tile0[j] = tiles;
+    bt.src[j] = static_cast<const uint16_t*>(J.src);
+    bt.dst[j] = static_cast<uint16_t*>(J.dst);
+    bt.rows[j] = J.rows;
+    bt.cols[j] = J.cols;
+    bt.ld[j] = J.src_ld;
+    tiles += (int64_t)(J.rows / 64) * (J.cols / 64);
+  }
+  bt.tile0[n] = tiles;
+  if (tiles == 0) return GLT_OK;
+  GLT_CHECK(tiles < (1ll << 33), GLT_ERR_SHAPE, "transpose16_batch: %lld tiles", (long long)tiles);
+  GLT_LAUNCH("transpose16", transpose16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, bt);
+  GLT_LAUNCH_CHECK("transpose16");
+  return GLT_OK;
+}
+
+glt_status transpose_batch(const T16Job* jobs, int n, int dtype, hipStream_t st) {
+  bool fast = dtype == GLT_DTYPE_BF16;
+  for (int j = 0; fast && j < n; ++j) fast = t16_ok(jobs[j].src, jobs[j].dst, jobs[j].rows, jobs[j].cols, jobs[j].src_ld);
+  if (fast) return transpose16_batch(jobs, n, st);
+  for (int j = 0; j < n; ++j) {
+    const glt_status s = transpose_any(jobs[j].src, jobs[j].dst, jobs[j].rows, jobs[j].cols, jobs[j].src_ld, dtype, st);
+    if (s != GLT_OK) return s;
+  }
+  return GLT_OK;
+}
+
 template <typename Tin, typename Tout>
 static glt_status launch_transpose(const Tin* src, Tout* dst, int rows, int cols, int64_t src_ld,
                                    hipStream_t st) {
   if (rows == 0 || cols == 0) return GLT_OK;
   if constexpr (sizeof(Tin) == 2 && sizeof(Tout) == 2) {
-    const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
-    if (al && rows % 64 == 0 && cols % 64 == 0 && src_ld % 8 == 0) {
-      const int64_t tiles = (int64_t)(rows / 64) * (cols / 64);
-      GLT_CHECK(tiles < (1ll << 33), GLT_ERR_SHAPE, "transpose: %lld tiles", (long long)tiles);
-      GLT_LAUNCH("transpose16", transpose16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, src, dst, rows,
-                 cols, src_ld);
-      GLT_LAUNCH_CHECK("transpose16");
-      return GLT_OK;
+    if (t16_ok(src, dst, rows, cols, src_ld)) {
+      const T16Job job{src, dst, rows, cols, src_ld};
+      return transpose16_batch(&job, 1, st);
     }
   }
   dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64));

@@ -353,23 +353,45 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
     uint16_t* DYS = reinterpret_cast<uint16_t*>(W + L.dyt);
     if ((s = shuffle_b(x, dt, D, true, D, M, XS, st)) != GLT_OK) return s;
     if ((s = shuffle_b(dy, dt, D, true, D, M, DYS, st)) != GLT_OK) return s;
+    const size_t es = esize(dt);
+    // every slice transpose first, batched into few launches
+    {
+      T16Job jobs[kMaxT16Jobs];
+      int nj = 0;
+      for (int j = 0; j < d->n_slices; ++j) {
+        const glt_graft_slice& sl = d->slices[j];
+        const glt_graft_grads& gr = grads[j];
+        char* base = W + L.slice0 + (size_t)j * L.slice_stride;
+        const size_t blk = align256((size_t)sl.s * M * es);
+        const char* srcs[3] = {static_cast<const char*>(dg), static_cast<const char*>(du),
+                               static_cast<const char*>(inter)};
+        const float* outs[3] = {gr.gate, gr.up, gr.down};
+        const float* mast[3] = {sl.master_gate, sl.master_up, sl.master_down};
+        for (int p = 0; p < 3; ++p) {
+          if (!outs[p] || !mast[p]) continue;
+          jobs[nj++] = T16Job{srcs[p] + (size_t)sl.i_start * es, base + p * blk, M, sl.s, (int64_t)N};
+          if (nj == kMaxT16Jobs) {
+            if ((s = transpose_batch(jobs, nj, dt, st)) != GLT_OK) return s;
+            nj = 0;
+          }
+        }
+      }
+      if (nj > 0 && (s = transpose_batch(jobs, nj, dt, st)) != GLT_OK) return s;
+    }
     GemmPlan plan;
     plan.label = "wgrad";
     plan.a_kind = LD_BF16;
     plan.b_kind = LD_SHUF;
-    const size_t es = esize(dt);
     for (int j = 0; j < d->n_slices; ++j) {
       const glt_graft_slice& sl = d->slices[j];
       const glt_graft_grads& gr = grads[j];
       char* base = W + L.slice0 + (size_t)j * L.slice_stride;
       const size_t blk = align256((size_t)sl.s * M * es);
-      char* srcs[3] = {static_cast<char*>(dg), static_cast<char*>(du), (char*)inter};
       float* outs[3] = {gr.gate, gr.up, gr.down};
       const float* mast[3] = {sl.master_gate, sl.master_up, sl.master_down};
       for (int p = 0; p < 3; ++p) {
         if (!outs[p] || !mast[p]) continue;
         char* AT = base + p * blk;
-        if ((s = transpose_any(srcs[p] + (size_t)sl.i_start * es, AT, M, sl.s, N, dt, st)) != GLT_OK) return s;
         if (plan.args.nprob == kMaxProb) {
           if ((s = run_gemm(plan, st)) != GLT_OK) return s;
           plan = GemmPlan();
