@@ -79,13 +79,20 @@ __global__ void __launch_bounds__(256) shuffle_kernel(const TS* __restrict__ src
 // n0 + 8 cb + c holding K = k0 + 8 kb .. +7, which is chunk (substep kb/2,
 // lane (8 cb + c) % 32 + 32 (kb & 1)) of its block. The chunks go to their
 // place in the wavefront's 8 KB of LDS and leave as contiguous 1 KB stores.
-__global__ void __launch_bounds__(256) shuffle_tr16_kernel(const uint16_t* __restrict__ src, int64_t ld, int rows,
-                                                           int K, uint16_t* __restrict__ dst) {
+__global__ void __launch_bounds__(256) shuffle_tr16_kernel(const uint16_t* __restrict__ src0,
+                                                           const uint16_t* __restrict__ src1, int64_t ld, int rows,
+                                                           int K, int njobs, uint16_t* __restrict__ dst0,
+                                                           uint16_t* __restrict__ dst1) {
   __shared__ __attribute__((aligned(16))) uint16_t stage[4][2 * kShufBlock];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  int64_t tile = (int64_t)blockIdx.x * 4 + wave;
   const int kt = K / 64;
-  if (tile >= (int64_t)(rows / 64) * kt) return;
+  const int64_t per = (int64_t)(rows / 64) * kt;  // tiles of one matrix; a second one of the same shape follows
+  if (tile >= per * njobs) return;
+  const bool second = tile >= per;
+  if (second) tile -= per;
+  const uint16_t* __restrict__ src = second ? src1 : src0;
+  uint16_t* __restrict__ dst = second ? dst1 : dst0;
   const int nt = (int)(tile / kt), ktile = (int)(tile % kt);
   const int n0 = nt * 64, k0 = ktile * 64;
   const int cb = lane & 7, kb = lane >> 3;
@@ -119,6 +126,24 @@ __global__ void __launch_bounds__(256) shuffle_tr16_kernel(const uint16_t* __res
   }
 }
 
+glt_status shuffle_b_tr_pair(const void* src0, const void* src1, int src_dtype, int64_t ld, int rows, int K,
+                            uint16_t* dst0, uint16_t* dst1, hipStream_t st) {
+  const bool fast = src_dtype == GLT_DTYPE_BF16 && rows > 0 && K > 0 && rows % 64 == 0 && K % 64 == 0 && ld % 8 == 0 &&
+                    src0 && src1 && dst0 && dst1 &&
+                    ((reinterpret_cast<uintptr_t>(src0) | reinterpret_cast<uintptr_t>(src1) |
+                      reinterpret_cast<uintptr_t>(dst0) | reinterpret_cast<uintptr_t>(dst1)) & 15) == 0;
+  if (!fast) {
+    const glt_status s = shuffle_b(src0, src_dtype, ld, true, rows, K, dst0, st);
+    return s != GLT_OK ? s : shuffle_b(src1, src_dtype, ld, true, rows, K, dst1, st);
+  }
+  const int64_t tiles = 2 * (int64_t)(rows / 64) * (K / 64);
+  GLT_CHECK(tiles < (1ll << 33), GLT_ERR_SHAPE, "shuffle_b_tr_pair: %lld tiles", (long long)tiles);
+  GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st,
+             static_cast<const uint16_t*>(src0), static_cast<const uint16_t*>(src1), ld, rows, K, 2, dst0, dst1);
+  GLT_LAUNCH_CHECK("shuffle_tr");
+  return GLT_OK;
+}
+
 glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed, int rows, int K, uint16_t* dst,
                      hipStream_t st) {
   GLT_CHECK(rows >= 0 && K >= 0, GLT_ERR_SHAPE, "shuffle_b: negative shape");
@@ -137,8 +162,8 @@ glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed
     if (transposed && rows % 64 == 0 && K % 64 == 0 && ld % 8 == 0 &&
         ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
       const int64_t tiles = (int64_t)(rows / 64) * (K / 64);
-      GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, s, ld, rows, K,
-                 dst);
+      GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, s, s, ld, rows,
+                 K, 1, dst, dst);
       GLT_LAUNCH_CHECK("shuffle_tr");
       return GLT_OK;
     }

@@ -62,6 +62,11 @@ inline int64_t prep_bytes(int I, int D) { return prep_offset(I, D, 6) * 2; }
 // Writes the shuffled form of B[rows, K]. Source element (r, k) is
 // src[r*ld + k] (transposed = false) or src[k*ld + r] (transposed = true);
 // src_dtype GLT_DTYPE_BF16 or GLT_DTYPE_F32 (rounded to bf16, RNE).
+// Two transposed operands of one shape (B[n][k] = src[k][n], rows x K) into
+// the fragment layout in one launch when they are bf16 in whole 64 x 64
+// tiles, else two shuffle_b calls.
+glt_status shuffle_b_tr_pair(const void* src0, const void* src1, int src_dtype, int64_t ld, int rows, int K,
+                            uint16_t* dst0, uint16_t* dst1, hipStream_t st);
 glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed, int rows, int K, uint16_t* dst,
                      hipStream_t st);
 

@@ -351,8 +351,7 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
     // B operands [D rows, K = M] once for all slices.
     uint16_t* XS = reinterpret_cast<uint16_t*>(W + L.xt);
     uint16_t* DYS = reinterpret_cast<uint16_t*>(W + L.dyt);
-    if ((s = shuffle_b(x, dt, D, true, D, M, XS, st)) != GLT_OK) return s;
-    if ((s = shuffle_b(dy, dt, D, true, D, M, DYS, st)) != GLT_OK) return s;
+    if ((s = shuffle_b_tr_pair(x, dy, dt, D, D, M, XS, DYS, st)) != GLT_OK) return s;
     const size_t es = esize(dt);
     // every slice transpose first, batched into few launches
     {
