@@ -33,6 +33,7 @@ M, D, I, S = 16384, 4096, 14336, 1024
 N = I + S
 EPS = 1e-5
 LR, B1, B2, AEPS, WD = 1e-4, 0.9, 0.999, 1e-8, 0.01
+CLIP = 1.0  # the reference's per-step global gradient clip (src/config.hpp:85)
 
 # algorithmic work per launch (FLOP) of each GEMM kernel of one step
 GEMM_FLOP = {
@@ -69,7 +70,7 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer measurement")
     ap.add_argument("--layer-only", action="store_true",
                     help="only the attention kernel and decoder-layer measurements (for profiling them alone)")
-    ap.add_argument("--cpu-tokens", type=int, default=1536)
+    ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (scale for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -133,6 +134,8 @@ def main():
     gptr = F.ptr_array([grads.data_ptr()])
     mptr, vptr = F.ptr_array([adam_m.data_ptr()]), F.ptr_array([adam_v.data_ptr()])
     pkptr = F.ptr_array([packed.data_ptr()])
+    clip_ws_bytes = lib.glt_adamw_workspace_size(0)
+    clip_ws = torch.empty(clip_ws_bytes, dtype=torch.uint8, device=dev)
 
     def step(i):
         F.call("glt_rmsnorm_fwd", p(x_raw), p(gamma), p(x), p(var), M, D, EPS, sp)
@@ -140,7 +143,8 @@ def main():
         F.call("glt_mlp_bwd", ctypes.byref(desc), ctypes.byref(base), p(x), p(dy), p(g), p(u), p(inter), p(dx), gg,
                p(ws), ws_bytes, sp)
         F.call("glt_rmsnorm_bwd", p(dx), p(x_raw), p(gamma), p(var), p(dx_raw), M, D, EPS, sp)
-        F.call("glt_adamw_graft_step", sl, 1, gptr, mptr, vptr, pkptr, 7, i, LR, B1, B2, AEPS, WD, sp)
+        F.call("glt_adamw_graft_step", sl, 1, gptr, mptr, vptr, pkptr, 7, i, LR, B1, B2, AEPS, WD, CLIP, p(clip_ws),
+               clip_ws_bytes, sp)
 
     if args.layer_only:
         out = {"attention": bench_attention(torch, F, sp, p),
@@ -181,13 +185,20 @@ def main():
     dom = max((k for k in kernels if k in GEMM_FLOP), key=lambda k: kernels[k]["ms_per_step"])
     dom_flop = GEMM_FLOP[dom] / kernels[dom]["launches_per_step"]  # per launch
     achieved = dom_flop / (kernels[dom]["avg_ms"] * 1e-3) / 1e12
-    traffic = None
+    # HBM bytes per launch are not measured in this run: hardware counters
+    # need a rocprofv3 --pmc run of their own. The figure is that run's
+    # (profiles/traffic_<kernel>.json, FETCH_SIZE and WRITE_SIZE passes
+    # scaled by a copy of known size; commands in
+    # profiles/mlp_step_llama3_8b_traffic.md), labelled as such.
+    traffic, traffic_source = None, None
     tf = os.path.join(ROOT, "profiles", f"traffic_{dom}.json")
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+        traffic_source = (f"profiles/traffic_{dom}.json: separate rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs "
+                          f"of this bench (commands in profiles/mlp_step_llama3_8b_traffic.md), not this run")
     roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                "flop_per_launch": dom_flop}
+                "traffic_source": traffic_source, "flop_per_launch": dom_flop}
 
     # HBM-bound kernels against the HBM roofline: RMSNorm and AdamW of the
     # step, RoPE at the decoder-layer shape (2 x 4096 tokens, 32 q / 8 kv
@@ -274,10 +285,11 @@ def bench_rope(torch, F, sp, p, reps=20):
 
 def bench_eval_stats(torch, F, sp, p, reps=3):
     """Shadow-eval statistics (CE sum and count, logit sum and sum of
-    squares, chained per-row FNV-1a hashes) over 4 x 4096 rows of the
-    Llama-3 vocabulary, bf16 logits; algorithmic bytes: logits read once.
-    Each row's hash chains every byte of the row, so a row is one thread's
-    sequential walk."""
+    squares, and the reference's FNV-1a hash chained over every logit byte)
+    over 4 x 4096 rows of the Llama-3 vocabulary, bf16 logits; algorithmic
+    bytes: logits read once. The exact hash takes three more passes over the
+    logits (its low-byte chain in two nibble passes, then the affine pass),
+    so the kernels read the logits five times; all of them are timed."""
     B, T, V = CE_B, CE_T, CE_V
     logits = torch.empty((B, T, V), dtype=torch.bfloat16, device="cuda")
     F.call("glt_fill_normal", p(logits), F.DTYPE_BF16, logits.numel(), 501, 0, 0.0, 3.0, sp)
@@ -287,7 +299,8 @@ def bench_eval_stats(torch, F, sp, p, reps=3):
     res = F.EvalResult()
 
     def run():
-        F.call("glt_eval_stats", p(logits), V, p(ids), B, T, V, ctypes.byref(res), p(ws), nbytes_ws, sp)
+        F.call("glt_eval_stats", p(logits), V, p(ids), B, T, V, F.EVAL_HASH_REFERENCE, F.FNV_BASIS, ctypes.byref(res),
+               p(ws), nbytes_ws, sp)
 
     run()
     torch.cuda.synchronize()
@@ -295,9 +308,9 @@ def bench_eval_stats(torch, F, sp, p, reps=3):
     for _ in range(reps):
         run()
     torch.cuda.synchronize()
-    tot, cnt = F.profile_collect().get("eval_rows", (0.0, 1))
+    prof = F.profile_collect()
     F.call("glt_profile_enable", 0)
-    t = tot / cnt
+    t = sum(tot for k, (tot, cnt) in prof.items() if k.startswith("eval_")) / reps
     nbytes = 2 * B * T * V
     del logits
     return {"bytes": nbytes, "ms": round(t, 4), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
@@ -513,38 +526,87 @@ def bench_bake(torch, F, lib, dev, sp, p, L=32, reps=5):
             "kernel_ms": round(kern_ms, 4), "launches": prof.get("bake", (0, 0))[1]}
 
 
+def _torch_cpu_step(torch, x_raw, gamma, Wg, Wu, Wd, masters, dy, adam):
+    """One step of the grafted layer in PyTorch on the CPU: the reference's
+    explicit-injection graft math with ATen ops, in the config's dtype where
+    the reference is bf16 and in f32 where it is f32:
+    RMSNorm (grafting.hip:116-146); base gate/up F.linear in bf16 (at::linear,
+    src/layer_forward_impl.inc:72, :122); the slice's f32 expand output of
+    bf16 operands injected into the bf16 pre-activations (appended slice:
+    onto zero base rows, src/kernels_elementwise_impl.inc:314-326); SiLU*up;
+    base down in bf16 plus the f32 contract term; the graft-only backward with
+    the f32 base GEMMs against f32 weight copies and bf16 graft GEMMs
+    (src/layer_backward_impl.inc:45-361); RMSNorm backward
+    (src/kernels_rmsnorm_kernels.inc:70-126); AdamW on the f32 masters
+    (src/kernels_optimizer_impl.inc:27-51). Masters are updated in place."""
+    F_ = torch.nn.functional
+    bf = torch.bfloat16
+    Dg, Du, Dd = masters
+    x = x_raw.float()
+    var = x.pow(2).mean(-1, keepdim=True)
+    r = torch.rsqrt(var + EPS)
+    w = gamma.float()
+    xn = (x * r * w).to(bf)
+    xf = xn.float()
+    dgb, dub, ddb = (t.to(bf).float() for t in (Dg, Du, Dd))
+    g = torch.cat([F_.linear(xn, Wg), (xf @ dgb.t()).to(bf)], 1).float()
+    u = torch.cat([F_.linear(xn, Wu), (xf @ dub.t()).to(bf)], 1).float()
+    inter = (F_.silu(g) * u).to(bf)
+    _y = (F_.linear(inter[:, :I], Wd).float() + inter[:, I:].float() @ ddb).to(bf)
+    # graft-only backward
+    dyf = dy.float()
+    dyb = dy.to(bf).float()
+    gi = torch.cat([dyf @ Wd.float(), dyb @ ddb.t()], 1)
+    grad_d = inter[:, I:].float().t() @ dyb
+    sg = torch.sigmoid(g)
+    dg = gi * u * sg * (1 + g * (1 - sg))
+    du = gi * g * sg
+    dgs, dus = dg[:, I:].to(bf).float(), du[:, I:].to(bf).float()
+    grad_g, grad_u = dgs.t() @ xf, dus.t() @ xf
+    dxn = dg[:, :I] @ Wg.float() + du[:, :I] @ Wu.float() + dgs @ dgb + dus @ dub
+    mean = (dxn * x * w).mean(-1, keepdim=True)
+    dx_raw = dxn * r * w - x * mean * r.pow(3)
+    for p_, grad_, (m_, v_) in zip((Dg, Du, Dd), (grad_g, grad_u, grad_d), adam):
+        m_.mul_(B1).add_(grad_, alpha=1 - B1)
+        v_.mul_(B2).addcmul_(grad_, grad_, value=1 - B2)
+        p_.sub_(LR * (m_ / (1 - B1)) / ((v_ / (1 - B2)).sqrt() + AEPS) + LR * WD * p_)
+    return dx_raw
+
+
 def cpu_baseline(torch, T, wg, wu, wd, masters, x_raw, gamma, dy):
-    """The oracle (C restatement of the reference path, f64 accumulation,
-    OpenMP) on the first T tokens of the same step: RMSNorm fwd, grafted MLP
-    fwd, graft-only bwd, RMSNorm bwd, AdamW."""
-    import numpy as np
-    from oracle import oracle as O
-    log(f"[bench] cpu baseline on {T} tokens")
-    h = lambda t: t.float().cpu().numpy()
-    Wg, Wu, Wd = h(wg), h(wu), h(wd)
-    ms = h(masters).reshape(3, S, D)
-    xr, gm, dyy = h(x_raw[:T]), h(gamma), h(dy[:T])
-    sl = [{"i0": I, "s": S, "h0": 0, "h": D, "gate": ms[0], "up": ms[1], "down": ms[2]}]
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    t0 = time.perf_counter()
-    xn, var = O.rmsnorm_fwd(xr, gm, EPS)
-    g, u, inter, y = O.mlp_fwd(xn, Wg, Wu, Wd, N, sl)
-    dxn, grads = O.mlp_bwd(xn, Wg, Wu, Wd, N, sl, g, u, inter, dyy)
-    O.rmsnorm_bwd(dxn, xr, gm, var, EPS)
-    for q in range(3):
-        O.adamw(ms[q], grads[0][q], np.zeros_like(ms[q]), np.zeros_like(ms[q]), 0, LR, B1, B2, AEPS, WD)
-    dt = time.perf_counter() - t0
-    cpu_model = ""
+    """The grafted layer step in PyTorch on the host cores (bf16, the
+    config's dtype), on the first T tokens of the same synthetic inputs:
+    RMSNorm, grafted MLP forward, graft-only backward, RMSNorm backward,
+    AdamW. One warmup step, then the median of three."""
+    import platform
+    import subprocess
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    log(f"[bench] cpu baseline: PyTorch CPU on {T} tokens, {torch.get_num_threads()} threads")
+    c = lambda t: t.detach().cpu()
+    Wg, Wu, Wd, gm = c(wg), c(wu), c(wd), c(gamma)
+    ms = c(masters).reshape(3, S, D).clone()
+    xr, dyy = c(x_raw[:T]), c(dy[:T])
+    adam = [(torch.zeros(S, D), torch.zeros(S, D)) for _ in range(3)]
+    times = []
+    for rep in range(4):
+        t0 = time.perf_counter()
+        _torch_cpu_step(torch, xr, gm, Wg, Wu, Wd, [ms[0], ms[1], ms[2]], dyy, adam)
+        if rep:
+            times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    cpu_model = platform.processor()
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
                 cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
+    except (OSError, subprocess.SubprocessError):
         pass
-    return {"value": round(T / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(T / dt, 2), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{T} of the {M} tokens of one step (RMSNorm, grafted MLP fwd, graft-only bwd, RMSNorm bwd, "
-                      f"AdamW), {dt:.2f} s; C oracle with f64 accumulation, {threads} OpenMP threads on {cpu_model}"}
+                      f"AdamW), median of 3 steps {dt:.2f} s; PyTorch {torch.__version__} CPU in bf16, "
+                      f"{torch.get_num_threads()} threads (os.cpu_count() = {threads}) on {cpu_model}"}
 
 
 if __name__ == "__main__":

@@ -18,7 +18,9 @@ STATUS_NAMES = {
     11: "GLT_ERR_FORMAT", 12: "GLT_ERR_NOT_FOUND",
 }
 DTYPE_BF16, DTYPE_F32, DTYPE_F16 = 0, 1, 2
-MLP_EXPLICIT, MLP_RECOMPUTE, MLP_RESIDUAL = 1, 2, 4
+MLP_EXPLICIT, MLP_RECOMPUTE, MLP_RESIDUAL, MLP_DY_F32 = 1, 2, 4, 8
+FNV_BASIS = 1469598103934665603
+EVAL_HASH_REFERENCE, EVAL_HASH_ROWS = 0, 1
 BAKE_IN_PLACE, BAKE_MATERIALIZE = 0, 1
 GEMM_EXPAND_FWD, GEMM_CONTRACT_FWD, GEMM_EXPAND_WGRAD, GEMM_CONTRACT_WGRAD, GEMM_EXPAND_IGRAD, \
     GEMM_CONTRACT_IGRAD = range(6)
@@ -129,7 +131,7 @@ SIGNATURES = {
                               _vp]),
     "glt_adamw_graft_step": (_i32, [ctypes.POINTER(GraftSlice), _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                     ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i32, _i32, _f32, _f32, _f32, _f32,
-                                    _f32, _vp]),
+                                    _f32, _f32, _vp, _sz, _vp]),
     "glt_shadow_bake": (_i32, [ctypes.POINTER(BakeDesc), ctypes.POINTER(ModelState), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), _vp]),
@@ -141,7 +143,8 @@ SIGNATURES = {
     "glt_model_fwd_workspace_size": (_sz, [ctypes.POINTER(Model)]),
     "glt_model_fwd": (_i32, [ctypes.POINTER(Model), _vp, _vp, _vp, _sz, _vp]),
     "glt_eval_stats_workspace_size": (_sz, [_i32, _i32]),
-    "glt_eval_stats": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, ctypes.POINTER(EvalResult), _vp, _sz, _vp]),
+    "glt_eval_stats": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _i32, ctypes.c_uint64, ctypes.POINTER(EvalResult),
+                              _vp, _sz, _vp]),
     "glt_st_open": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "glt_st_close": (None, [_vp]),
     "glt_st_count": (_i32, [_vp]),

@@ -1,5 +1,6 @@
 // AdamW over graft parameters with the optional global-L2 gradient clip and
 // the bf16 mirror refresh fused into the update.
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -9,15 +10,25 @@ namespace glt {
 
 
 constexpr int kClipBlocks = 1024;
+constexpr int kClipMaxSegs = 24;  // 3 projections x up to 8 slices
 
-// Partial sums of g^2 (f32, like the reference reduce_l2_kernel,
-// src/kernels_elementwise_impl.inc:141-165), one partial per workgroup.
-__global__ void __launch_bounds__(256) sumsq_partial_kernel(const float* __restrict__ g, int64_t n,
-                                                            float* __restrict__ partial) {
+// The gradient vectors one clip norm covers: partial sums of g^2 (f32, like
+// the reference reduce_l2_kernel, src/kernels_elementwise_impl.inc:141-165),
+// one partial per workgroup over every listed vector.
+struct ClipSegs {
+  const float* g[kClipMaxSegs];
+  int64_t n[kClipMaxSegs];
+  int nseg;
+};
+
+__global__ void __launch_bounds__(256) sumsq_partial_kernel(const ClipSegs segs, float* __restrict__ partial) {
   __shared__ float wsum[4];
   float s = 0.f;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) s += g[i] * g[i];
+  for (int j = 0; j < segs.nseg; ++j) {
+    const float* g = segs.g[j];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < segs.n[j]; i += stride) s += g[i] * g[i];
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
@@ -26,12 +37,33 @@ __global__ void __launch_bounds__(256) sumsq_partial_kernel(const float* __restr
 }
 
 // scale = clip/norm if norm > clip else 1, norm = sqrt(sum + 1e-8)
-// (reference calc_scale_kernel, src/kernels_elementwise_impl.inc:193-196).
-__device__ __forceinline__ float clip_scale(const float* partial, int np, float clip) {
+// (reference calc_scale_kernel, src/kernels_elementwise_impl.inc:170-197):
+// one workgroup adds the partials in a fixed order and writes the scale.
+__global__ void __launch_bounds__(256) clip_scale_kernel(const float* __restrict__ partial, int np, float clip,
+                                                         float* __restrict__ scale) {
+  __shared__ float wsum[4];
   float s = 0.f;
-  for (int i = 0; i < np; ++i) s += partial[i];
-  const float norm = sqrtf(s + 1e-8f);
-  return norm > clip ? clip / norm : 1.0f;
+  for (int i = threadIdx.x; i < np; i += 256) s += partial[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float norm = sqrtf(wsum[0] + wsum[1] + wsum[2] + wsum[3] + 1e-8f);
+    scale[0] = norm > clip ? clip / norm : 1.0f;
+  }
+}
+
+// Launches the two clip kernels over segs; scale lands in ws[kClipBlocks].
+glt_status launch_clip(const ClipSegs& segs, float clip, float* ws, hipStream_t st) {
+  int64_t total = 0;
+  for (int j = 0; j < segs.nseg; ++j) total += segs.n[j];
+  const int np = (int)std::max<int64_t>(1, std::min<int64_t>(kClipBlocks, cdiv(total, 256)));
+  GLT_LAUNCH("clip_sumsq", sumsq_partial_kernel, dim3(np), dim3(256), 0, st, segs, ws);
+  GLT_LAUNCH_CHECK("sumsq_partial");
+  GLT_LAUNCH("clip_scale", clip_scale_kernel, dim3(1), dim3(256), 0, st, ws, np, clip, ws + kClipBlocks);
+  GLT_LAUNCH_CHECK("clip_scale");
+  return GLT_OK;
 }
 
 // One AdamW element update in the reference's operation order
@@ -49,14 +81,8 @@ __global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ w, const
                                                     float* __restrict__ m, float* __restrict__ v,
                                                     uint16_t* __restrict__ mirror, int64_t n, float lr,
                                                     float b1, float b2, float b1c, float b2c, float eps,
-                                                    float wd, const float* __restrict__ partial, int np,
-                                                    float clip) {
-  __shared__ float s_scale;
-  if (partial) {
-    if (threadIdx.x == 0) s_scale = clip_scale(partial, np, clip);
-    __syncthreads();
-  }
-  const float scale = partial ? s_scale : 1.0f;
+                                                    float wd, const float* __restrict__ clip_scale) {
+  const float scale = clip_scale ? *clip_scale : 1.0f;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     float mi = m[i], vi = v[i];
@@ -79,9 +105,11 @@ __global__ void __launch_bounds__(256) adamw_pack_kernel(float* __restrict__ w, 
                                                          float* __restrict__ m, float* __restrict__ v, int S,
                                                          int H, float lr, float b1, float b2, float b1c,
                                                          float b2c, float eps, float wd,
+                                                         const float* __restrict__ clip_scale,
                                                          uint16_t* __restrict__ rm, uint16_t* __restrict__ rmt,
                                                          uint16_t* __restrict__ sh, uint16_t* __restrict__ sht) {
   __shared__ float tile[64][65];
+  const float scale = clip_scale ? *clip_scale : 1.0f;
   const int hb = H / 64;
   const int r0 = (blockIdx.x / hb) * 64, c0 = (blockIdx.x % hb) * 64;
   const int t = threadIdx.x;
@@ -97,7 +125,7 @@ __global__ void __launch_bounds__(256) adamw_pack_kernel(float* __restrict__ w, 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float a = mi[e], b = vi[e];
-        nw[e] = adamw_elem(wi[e], gi[e], a, b, lr, b1, b2, b1c, b2c, eps, wd);
+        nw[e] = adamw_elem(wi[e], gi[e] * scale, a, b, lr, b1, b2, b1c, b2c, eps, wd);
         mi[e] = a;
         vi[e] = b;
         tile[r][c4 + e] = nw[e];
@@ -160,7 +188,7 @@ using namespace glt;
 
 extern "C" {
 
-size_t glt_adamw_workspace_size(int64_t n) { return (size_t)kClipBlocks * sizeof(float); }
+size_t glt_adamw_workspace_size(int64_t n) { return (size_t)(kClipBlocks + 64) * sizeof(float); }
 
 glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* mirror, int64_t n, int32_t step,
                           float lr, float beta1, float beta2, float eps, float weight_decay, float clip_norm,
@@ -169,33 +197,62 @@ glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* mirr
   GLT_CHECK(n == 0 || (w && g && m && v), GLT_ERR_INVALID_ARG, "glt_adamw_step: null pointer");
   if (n == 0) return GLT_OK;
   hipStream_t st = as_stream(stream);
-  float* partial = nullptr;
-  int np = 0;
+  const float* scale = nullptr;
   if (clip_norm > 0.f) {
     GLT_CHECK(ws && ws_bytes >= glt_adamw_workspace_size(n), GLT_ERR_WORKSPACE,
               "glt_adamw_step: clip needs %zu workspace bytes", glt_adamw_workspace_size(n));
-    partial = static_cast<float*>(ws);
-    np = (int)std::min<int64_t>(kClipBlocks, cdiv(n, 256));
-    GLT_LAUNCH("clip_sumsq", sumsq_partial_kernel, dim3(np), dim3(256), 0, st, g, n, partial);
-    GLT_LAUNCH_CHECK("sumsq_partial");
+    ClipSegs segs{};
+    segs.g[0] = g;
+    segs.n[0] = n;
+    segs.nseg = 1;
+    glt_status s = launch_clip(segs, clip_norm, static_cast<float*>(ws), st);
+    if (s != GLT_OK) return s;
+    scale = static_cast<const float*>(ws) + kClipBlocks;
   }
   // bias corrections as the reference computes them on the host
   // (src/kernels_optimizer_impl.inc:64-65)
   const float b1c = 1.0f / (1.0f - powf(beta1, (float)(step + 1)));
   const float b2c = 1.0f / (1.0f - powf(beta2, (float)(step + 1)));
   GLT_LAUNCH("adamw", adamw_kernel, dim3(grid_n(n)), dim3(256), 0, st, w, g, m, v, mirror, n, lr, beta1, beta2,
-                     b1c, b2c, eps, weight_decay, partial, np, clip_norm);
+                     b1c, b2c, eps, weight_decay, scale);
   GLT_LAUNCH_CHECK("adamw");
   return GLT_OK;
 }
 
-glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices, float* const* grads,
-                                float* const* m, float* const* v, uint16_t* const* packed_out,
-                                int32_t proj_mask, int32_t step, float lr, float beta1, float beta2,
-                                float eps, float weight_decay, void* stream) {
-  GLT_CHECK(n_slices >= 0 && (n_slices == 0 || (slices && grads && m && v)), GLT_ERR_INVALID_ARG,
-            "glt_adamw_graft_step: null pointer");
-  hipStream_t st = as_stream(stream);
+namespace glt {
+// The graft step over caller-provided clip memory (kClipBlocks + 1 floats).
+static glt_status graft_step(const glt_graft_slice* slices, int32_t n_slices, float* const* grads, float* const* m,
+                             float* const* v, uint16_t* const* packed_out, int32_t proj_mask, int32_t step, float lr,
+                             float beta1, float beta2, float eps, float weight_decay, float clip_norm,
+                             float* clip_ws, hipStream_t st) {
+  GLT_CHECK(n_slices >= 0 && n_slices <= kClipMaxSegs / 3, GLT_ERR_UNSUPPORTED,
+            "glt_adamw_graft_step: %d slices (max %d)", n_slices, kClipMaxSegs / 3);
+  GLT_CHECK(n_slices == 0 || (slices && grads && m && v), GLT_ERR_INVALID_ARG, "glt_adamw_graft_step: null pointer");
+  for (int j = 0; j < n_slices; ++j)
+    GLT_CHECK(grads[j] && m[j] && v[j], GLT_ERR_INVALID_ARG, "glt_adamw_graft_step: null state of slice %d", j);
+  const float* scale = nullptr;
+  if (clip_norm > 0.f) {
+    // the global L2 norm over every projection this step updates (the
+    // reference clips all of its L*3 deltas together, grafting.hip:1149-1164;
+    // the gradients of projections it does not graft stay zero)
+    ClipSegs segs{};
+    for (int j = 0; j < n_slices; ++j) {
+      const glt_graft_slice& sl = slices[j];
+      const int64_t sh = (int64_t)sl.s * sl.h;
+      const float* masters[3] = {sl.master_gate, sl.master_up, sl.master_down};
+      for (int p = 0; p < 3; ++p) {
+        if (!masters[p] || !(proj_mask & (1 << p))) continue;
+        segs.g[segs.nseg] = grads[j] + p * sh;
+        segs.n[segs.nseg] = sh;
+        ++segs.nseg;
+      }
+    }
+    if (segs.nseg > 0) {
+      glt_status s = launch_clip(segs, clip_norm, clip_ws, st);
+      if (s != GLT_OK) return s;
+      scale = clip_ws + kClipBlocks;
+    }
+  }
   const float b1c = 1.0f / (1.0f - powf(beta1, (float)(step + 1)));
   const float b2c = 1.0f / (1.0f - powf(beta2, (float)(step + 1)));
   for (int j = 0; j < n_slices; ++j) {
@@ -214,22 +271,33 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
         GLT_CHECK(tiles < (1ll << 31), GLT_ERR_SHAPE, "glt_adamw_graft_step: %lld tiles", (long long)tiles);
         uint16_t* rm = pk + 2 * p * sh;
         GLT_LAUNCH("adamw_pack", adamw_pack_kernel, dim3((unsigned)tiles), dim3(256), 0, st, w, gp, mp, vp,
-                   sl.s, sl.h, lr, beta1, beta2, b1c, b2c, eps, weight_decay, rm, rm + sh,
+                   sl.s, sl.h, lr, beta1, beta2, b1c, b2c, eps, weight_decay, scale, rm, rm + sh,
                    pk + packed_shuf_offset(sl.s, sl.h, 2 * p), pk + packed_shuf_offset(sl.s, sl.h, 2 * p + 1));
         GLT_LAUNCH_CHECK("adamw_pack");
         continue;
       }
-      GLT_LAUNCH("adamw", adamw_kernel, dim3(grid_n(sh)), dim3(256), 0, st, w, grads[j] + p * sh,
-                         m[j] + p * sh, v[j] + p * sh, (uint16_t*)nullptr, sh, lr, beta1, beta2, b1c, b2c, eps,
-                         weight_decay, (const float*)nullptr, 0, 0.f);
+      GLT_LAUNCH("adamw", adamw_kernel, dim3(grid_n(sh)), dim3(256), 0, st, w, gp, mp, vp, (uint16_t*)nullptr, sh,
+                 lr, beta1, beta2, b1c, b2c, eps, weight_decay, scale);
       GLT_LAUNCH_CHECK("adamw_graft");
-      if (packed_out && packed_out[j]) {
-        glt_status s = pack_projection(w, sl.s, sl.h, p, packed_out[j], st);
+      if (pk) {
+        glt_status s = pack_projection(w, sl.s, sl.h, p, pk, st);
         if (s != GLT_OK) return s;
       }
     }
   }
   return GLT_OK;
+}
+}  // namespace glt
+
+glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices, float* const* grads,
+                                float* const* m, float* const* v, uint16_t* const* packed_out,
+                                int32_t proj_mask, int32_t step, float lr, float beta1, float beta2,
+                                float eps, float weight_decay, float clip_norm, void* ws, size_t ws_bytes,
+                                void* stream) {
+  GLT_CHECK(clip_norm <= 0.f || (ws && ws_bytes >= glt_adamw_workspace_size(0)), GLT_ERR_WORKSPACE,
+            "glt_adamw_graft_step: clip needs %zu workspace bytes", glt_adamw_workspace_size(0));
+  return graft_step(slices, n_slices, grads, m, v, packed_out, proj_mask, step, lr, beta1, beta2, eps, weight_decay,
+                    clip_norm, static_cast<float*>(ws), as_stream(stream));
 }
 
 }  // extern "C"

@@ -24,6 +24,7 @@
 // & 1) and chunk c at c ^ ((R' >> 1) & 7)). Both the fragment reads and the
 // transposing writes are free of bank conflicts. Two stages, the next key
 // tile is loaded while the current one is consumed.
+#include <atomic>
 #include "common.hpp"
 
 namespace glt {
@@ -322,14 +323,15 @@ extern "C" glt_status glt_attention_fwd(const void* q, const void* k, const void
   // K rows are addressed through 31-bit buffer offsets
   GLT_CHECK((int64_t)B * T * Hkv * kHd * 2 < (int64_t)kOob, GLT_ERR_SHAPE, "glt_attention_fwd: K of %lld bytes",
             (long long)B * T * Hkv * kHd * 2);
-  // the dynamic-LDS limit is a per-device attribute of the kernel
-  static bool attr_set[64] = {};
+  // the dynamic-LDS limit is a per-device attribute of the kernel (set
+  // once per device; a concurrent first call sets the same value again)
+  static std::atomic<bool> attr_set[64];
   int dev = 0;
   GLT_TRY_HIP(hipGetDevice(&dev));
   GLT_CHECK(dev >= 0 && dev < 64, GLT_ERR_HIP, "glt_attention_fwd: device index %d out of range", dev);
-  if (!attr_set[dev]) {
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
     GLT_TRY_HIP(hipFuncSetAttribute((const void*)attn_fwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kAttnLds));
-    attr_set[dev] = true;
+    attr_set[dev].store(true, std::memory_order_release);
   }
   const float scale_log2 = scale * 1.4426950408889634f;
   // 1-D over (query block, batch, head)

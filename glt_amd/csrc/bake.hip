@@ -6,7 +6,7 @@
 // and, for the down projection, writes the transposed block with a row
 // stride of I elements per lane (uncoalesced).
 //
-// Here one launch covers up to kMaxLayers layers (grid.z) and has two kinds
+// Here one launch covers up to 16 layers (grid.z) and has two kinds
 // of workgroup:
 //  * stream blocks: each thread owns one 16-byte chunk (8 elements) of an
 //    output row, consecutive threads and workgroups walk consecutive chunks
@@ -24,8 +24,11 @@
 namespace glt {
 
 constexpr int kTile = 64;
-constexpr int kMaxLayers = 32;
-constexpr int kMaxBakeSlices = 4;
+// Layers per launch and slices per bake: the launch argument block carries a
+// graft pointer per (layer, slice), 1 KB at 16 x 8. Eight slices cover every
+// stack glt_mlp_fwd / glt_mlp_bwd take (at most 7).
+constexpr int kMaxLayers = 16;
+constexpr int kMaxBakeSlices = 8;
 
 struct BakePlacement {
   int i0, s, h0, h;

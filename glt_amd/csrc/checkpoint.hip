@@ -332,8 +332,10 @@ glt_status st_add_file(glt_st_set* s, const std::string& path) {
               kv.first.c_str());
     x.data = base + data0 + b.num;
     x.bytes = (size_t)(e.num - b.num);
+    // n is compared through a division first: the product n * esize could
+    // wrap around for a crafted shape and match a small byte count
     if (x.dtype >= 0)
-      GLT_CHECK(x.bytes == (size_t)n * st_esize(x.dtype), GLT_ERR_FORMAT,
+      GLT_CHECK((uint64_t)n <= x.bytes / st_esize(x.dtype) && x.bytes == (size_t)n * st_esize(x.dtype), GLT_ERR_FORMAT,
                 "glt_st_open: %s: tensor %s: %zu bytes for %lld elements", path.c_str(), kv.first.c_str(), x.bytes,
                 (long long)n);
     s->tensors.emplace(kv.first, std::move(x));
@@ -570,8 +572,17 @@ glt_status glt_st_read(const glt_st_set* s, const char* name, void* dst, int32_t
             "glt_st_read: destination dtype %d", dst_dtype);
   GLT_CHECK(!transpose || t->shape.size() == 2, GLT_ERR_SHAPE, "glt_st_read: transpose of a %zu-dim tensor",
             t->shape.size());
+  // element count and output size with overflow checks (glt_st_open has
+  // already tied the count to the stored bytes; this keeps glt_st_read safe
+  // on its own)
   size_t n = 1;
-  for (int64_t d : t->shape) n *= (size_t)d;
+  for (int64_t d : t->shape) {
+    GLT_CHECK(d >= 0 && (d == 0 || n <= SIZE_MAX / (size_t)d), GLT_ERR_FORMAT, "glt_st_read: %s: shape overflows",
+              name);
+    n *= (size_t)d;
+  }
+  GLT_CHECK(n <= t->bytes / st_esize(t->dtype) && n <= SIZE_MAX / 4, GLT_ERR_FORMAT,
+            "glt_st_read: %s: %zu elements in %zu stored bytes", name, n, t->bytes);
   const size_t out_bytes = n * st_esize(dst_dtype);
   const unsigned char* src = t->data;
   std::vector<unsigned char> stage;

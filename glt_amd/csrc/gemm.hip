@@ -1,5 +1,6 @@
 // Segment-list GEMM kernels: the gfx950 bf16 MFMA kernel and the strided
 // generic kernel (f32 path, unaligned shapes, graft-GEMM probes).
+#include <atomic>
 #include <cmath>
 
 #include "gemm.hpp"
@@ -802,31 +803,38 @@ bool gemm_mfma_eligible(const GemmPlan& plan) {
 }
 
 // CUs of the current device (the persistent grid size), cached per device.
+// The caches are atomics: host threads making their first calls at the same
+// time may both query the device (the same value), never race on the slot.
 static glt_status device_cus(int& cus) {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64];
   int dev = 0;
   GLT_TRY_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= 64) {
     set_error("gemm: device index %d out of range", dev);
     return GLT_ERR_HIP;
   }
-  if (cached[dev] == 0) GLT_TRY_HIP(hipDeviceGetAttribute(&cached[dev], hipDeviceAttributeMultiprocessorCount, dev));
-  cus = cached[dev];
+  int c = cached[dev].load(std::memory_order_acquire);
+  if (c == 0) {
+    GLT_TRY_HIP(hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev));
+    cached[dev].store(c, std::memory_order_release);
+  }
+  cus = c;
   return GLT_OK;
 }
 
 template <typename TO, int MODE, bool DUAL>
 static glt_status launch_mfma(const GArgs& a, hipStream_t st, const char* label) {
-  // the dynamic-LDS limit is a per-device attribute of the kernel
-  static bool attr_set[64] = {};
+  // the dynamic-LDS limit is a per-device attribute of the kernel (set
+  // once per device; a concurrent first call sets the same value again)
+  static std::atomic<bool> attr_set[64];
   auto fn = gemm_mfma_kernel<TO, MODE, DUAL>;
   int dev = 0;
   GLT_TRY_HIP(hipGetDevice(&dev));
   GLT_CHECK(dev >= 0 && dev < 64, GLT_ERR_HIP, "gemm: device index %d out of range", dev);
-  if (!attr_set[dev]) {
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
     GLT_TRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLds));
-    attr_set[dev] = true;
+    attr_set[dev].store(true, std::memory_order_release);
   }
   int cus = 0;
   const glt_status rc = device_cus(cus);

@@ -103,17 +103,47 @@ struct Proj {
   int64_t N;
   void* out;
 };
+// The MFMA kernel addresses a tile's rows through 31-bit buffer offsets
+// from the operand base, so a projection whose output (or input) extent
+// passes 2 GiB (an LM head over 16384 tokens x 128256 logits is 4 GiB) runs
+// as row blocks of at most this many tokens, each on the MFMA kernel.
+int64_t project_rows_per_launch(int64_t K, const Proj* ps, int n) {
+  int64_t widest = K;
+  for (int j = 0; j < n; ++j) widest = std::max(widest, ps[j].N);
+  const int64_t rows = ((int64_t)kOob - 1) / (widest * 2) - 256;  // one tile of rows past the block
+  return rows / 256 * 256;
+}
+
 glt_status project(const void* A, int64_t M, int64_t K, const Proj* ps, int n, int mode, const char* label,
                    hipStream_t st) {
-  GemmPlan plan;
-  plan.label = label;
-  plan.a_kind = LD_BF16;
-  plan.b_kind = LD_SHUF;
-  for (int j = 0; j < n; ++j) {
-    plan.add_problem(prob(M, ps[j].N, mode, ps[j].out));
-    plan.add_seg(seg(A, K, (int)K, (int)ps[j].N, ps[j].shuf, shuf_k(K)));
+  auto mfma_plan = [&](int64_t r0, int64_t rows, GemmPlan& plan) {
+    plan.label = label;
+    plan.a_kind = LD_BF16;
+    plan.b_kind = LD_SHUF;
+    for (int j = 0; j < n; ++j) {
+      plan.add_problem(prob(rows, ps[j].N, mode, static_cast<char*>(ps[j].out) + r0 * ps[j].N * 2));
+      plan.add_seg(seg(static_cast<const char*>(A) + r0 * K * 2, K, (int)K, (int)ps[j].N, ps[j].shuf, shuf_k(K)));
+    }
+  };
+  {
+    GemmPlan plan;
+    mfma_plan(0, M, plan);
+    if (gemm_mfma_eligible(plan)) return run_gemm(plan, st);
   }
-  if (gemm_mfma_eligible(plan)) return run_gemm(plan, st);
+  const int64_t step = project_rows_per_launch(K, ps, n);
+  if (step >= 256 && M > step) {
+    GemmPlan first;
+    mfma_plan(0, step, first);
+    if (gemm_mfma_eligible(first)) {
+      for (int64_t r0 = 0; r0 < M; r0 += step) {
+        GemmPlan plan;
+        mfma_plan(r0, std::min(step, M - r0), plan);
+        const glt_status s = run_gemm(plan, st);
+        if (s != GLT_OK) return s;
+      }
+      return GLT_OK;
+    }
+  }
   GemmPlan gen;
   gen.label = label;
   gen.a_kind = gen.b_kind = LD_BF16;
@@ -231,10 +261,9 @@ __global__ void __launch_bounds__(256) embedding_kernel(const int32_t* ids, cons
   }
 }
 
-// Per-row eval terms, one thread per row, in row order within the row (the
-// hash is sequential): f64 sum / sum of squares of the f32 logits, FNV-1a of
-// their little-endian bytes, and for rows t < T-1 the f32 cross-entropy
-// max + log(sum exp(x - max)) - x_label against ids[b, t+1].
+// Per-row eval terms: f64 sum / sum of squares of the f32 logits, for rows
+// t < T-1 the f32 cross-entropy max + log(sum exp(x - max)) - x_label
+// against ids[b, t+1], and (rows hash form only) an FNV-1a hash of the row.
 struct EvalRow {
   double sum, sumsq;
   uint64_t hash;
@@ -244,30 +273,57 @@ struct EvalRow {
 // the reference's offset basis (grafting.hip:505): the published FNV-1a basis
 // 14695981039346656037 with its last digit missing; the hash is defined by it
 constexpr uint64_t kFnvBasis = 1469598103934665603ULL;
-constexpr uint64_t kFnvPrime = 1099511628211ULL;
+constexpr uint64_t kFnvPrime = 1099511628211ULL;  // 2^40 + 0x1B3
 
-// One workgroup per 16 rows, 16 threads per row: thread c of a row takes
-// chunk c of kEvalChunks chunks of ceil(V / kEvalChunks) logits (the last
-// ones shorter or empty) and accumulates its f64 sum and sum of squares,
-// its maximum and the FNV-1a hash of the chunk's f32 bytes (from the
-// basis). The row's threads then share their maxima through LDS, sum
-// exp(x - max) over their chunks, and thread 0 of the row adds the parts in
-// chunk order and hashes the chunk hashes' little-endian bytes in order.
+// Every row is cut into kEvalChunks chunks of ceil(V / kEvalChunks) logits
+// (the last ones shorter or empty); one thread walks one chunk in order.
 constexpr int kEvalChunks = 16;
 
-__device__ __forceinline__ void eval_elem(uint32_t h16, double& s, double& s2, float& mx, uint64_t& h) {
-  const uint32_t bits = h16 << 16;
-  const float f = __uint_as_float(bits);
-  s += f;
-  s2 += (double)f * f;
-  mx = fmaxf(mx, f);
+__device__ __forceinline__ void chunk_range(int V, int c, int& v0, int& v1) {
+  const int L = (V + kEvalChunks - 1) / kEvalChunks;
+  v0 = min(V, c * L);
+  v1 = min(V, v0 + L);
+}
+
+// Calls f(bits) for the bf16 logits x[v0, v1) in order: eight 16-byte loads
+// in flight per thread when the chunk is aligned, else one element a time.
+template <typename F>
+__device__ __forceinline__ void walk_chunk(const uint16_t* x, int v0, int v1, F&& f) {
+  const bool vec = ((reinterpret_cast<uintptr_t>(x + v0) & 15) == 0) && ((v1 - v0) % 8 == 0);
+  if (vec) {
+    int v = v0;
+    for (; v + 64 <= v1; v += 64) {
+      u32x4 q[8];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    h ^= (bits >> (8 * k)) & 0xFFu;
-    h *= kFnvPrime;
+      for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const u32x4*>(x + v + 8 * i);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f(q[i][e] & 0xFFFFu);
+          f(q[i][e] >> 16);
+        }
+    }
+    for (; v < v1; v += 8) {
+      const u32x4 q = *reinterpret_cast<const u32x4*>(x + v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f(q[e] & 0xFFFFu);
+        f(q[e] >> 16);
+      }
+    }
+  } else {
+    for (int v = v0; v < v1; ++v) f((uint32_t)x[v]);
   }
 }
 
+// One workgroup per 16 rows, 16 threads per row: thread c of a row takes
+// chunk c and accumulates its f64 sum and sum of squares, its maximum and
+// (ROW_HASH) the FNV-1a hash of the chunk's f32 bytes from the basis. The
+// row's threads then share their maxima through LDS, sum exp(x - max) over
+// their chunks, and thread 0 of the row adds the parts in chunk order and
+// (ROW_HASH) hashes the chunk hashes' little-endian bytes in order.
+template <bool ROW_HASH>
 __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, int64_t ld, const int32_t* ids, int B,
                                                         int T, int V, EvalRow* rows) {
   __shared__ float s_max[16][kEvalChunks], s_se[16][kEvalChunks];
@@ -276,41 +332,27 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
   const int lr = threadIdx.x >> 4, c = threadIdx.x & (kEvalChunks - 1);
   const int64_t r = (int64_t)blockIdx.x * 16 + lr;
   const bool valid = r < (int64_t)B * T;
-  const int L = (V + kEvalChunks - 1) / kEvalChunks;
-  const int v0 = min(V, c * L), v1 = min(V, v0 + L);
+  int v0, v1;
+  chunk_range(V, c, v0, v1);
   const uint16_t* x = logits + (valid ? r : 0) * ld;
-  const bool vec = ((reinterpret_cast<uintptr_t>(x + v0) & 15) == 0) && ((v1 - v0) % 8 == 0);
   double s = 0.0, s2 = 0.0;
   float mx = -INFINITY;
   uint64_t h = kFnvBasis;
-  if (valid) {
-    if (vec) {
-      // eight 16-byte loads in flight per thread, consumed in element order
-      int v = v0;
-      for (; v + 64 <= v1; v += 64) {
-        u32x4 q[8];
+  if (valid)
+    walk_chunk(x, v0, v1, [&](uint32_t h16) {
+      const uint32_t bits = h16 << 16;
+      const float f = __uint_as_float(bits);
+      s += f;
+      s2 += (double)f * f;
+      mx = fmaxf(mx, f);
+      if constexpr (ROW_HASH) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const u32x4*>(x + v + 8 * i);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            eval_elem(q[i][e] & 0xFFFFu, s, s2, mx, h);
-            eval_elem(q[i][e] >> 16, s, s2, mx, h);
-          }
-      }
-      for (; v < v1; v += 8) {
-        const u32x4 q = *reinterpret_cast<const u32x4*>(x + v);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          eval_elem(q[e] & 0xFFFFu, s, s2, mx, h);
-          eval_elem(q[e] >> 16, s, s2, mx, h);
+        for (int k = 0; k < 4; ++k) {
+          h ^= (bits >> (8 * k)) & 0xFFu;
+          h *= kFnvPrime;
         }
       }
-    } else {
-      for (int v = v0; v < v1; ++v) eval_elem(x[v], s, s2, mx, h);
-    }
-  }
+    });
   s_max[lr][c] = mx;
   __syncthreads();
   float rmx = -INFINITY;
@@ -319,33 +361,7 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
   const int b = valid ? (int)(r / T) : 0, t = valid ? (int)(r - (int64_t)b * T) : 0;
   const bool scored = valid && t < T - 1;
   float se = 0.f;
-  if (scored) {
-    if (vec) {
-      int v = v0;
-      for (; v + 64 <= v1; v += 64) {
-        u32x4 q[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const u32x4*>(x + v + 8 * i);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            se += expf(__uint_as_float(q[i][e] << 16) - rmx);
-            se += expf(__uint_as_float(q[i][e] & 0xFFFF0000u) - rmx);
-          }
-      }
-      for (; v < v1; v += 8) {
-        const u32x4 q = *reinterpret_cast<const u32x4*>(x + v);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          se += expf(__uint_as_float(q[e] << 16) - rmx);
-          se += expf(__uint_as_float(q[e] & 0xFFFF0000u) - rmx);
-        }
-      }
-    } else {
-      for (int v = v0; v < v1; ++v) se += expf(__uint_as_float((uint32_t)x[v] << 16) - rmx);
-    }
-  }
+  if (scored) walk_chunk(x, v0, v1, [&](uint32_t h16) { se += expf(__uint_as_float(h16 << 16) - rmx); });
   s_se[lr][c] = se;
   s_sum[lr][c] = s;
   s_sq[lr][c] = s2;
@@ -358,10 +374,12 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
     o.sum += s_sum[lr][k];
     o.sumsq += s_sq[lr][k];
     tse += s_se[lr][k];
-    const uint64_t hk = s_h[lr][k];
-    for (int j = 0; j < 8; ++j) {
-      o.hash ^= (hk >> (8 * j)) & 0xFFu;
-      o.hash *= kFnvPrime;
+    if constexpr (ROW_HASH) {
+      const uint64_t hk = s_h[lr][k];
+      for (int j = 0; j < 8; ++j) {
+        o.hash ^= (hk >> (8 * j)) & 0xFFu;
+        o.hash *= kFnvPrime;
+      }
     }
   }
   if (scored) {
@@ -371,6 +389,194 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
     o.scored = 1;
   }
   rows[r] = o;
+}
+
+// ------------------------------------------------ the reference's logits hash
+// The reference hashes every f32 logit's four little-endian bytes in (b, t, v)
+// order with one FNV-1a chain, h = (h ^ byte) * P mod 2^64 (grafting.hip:536-546),
+// continued across its eval batches. That chain is computed here exactly, in
+// parallel over the chunks of all rows (chunk k = row k / 16, part k % 16),
+// in three passes:
+//  * P is odd, so the low byte of h evolves on its own:
+//    s' = ((s ^ byte) * P) mod 256. Bit j of s' depends only on bits 0..j of
+//    s, so the low nibble is a 16-state chain. Pass 1 runs every chunk from
+//    all 16 low nibbles, giving each chunk's map of 16 nibbles; an ordered
+//    scan of the maps from the start hash's nibble gives every chunk's
+//    starting low nibble.
+//  * Pass 2 does the same for the high nibble of the low byte, each chunk's
+//    16 runs starting from its known low nibble.
+//  * With the low byte s of h known at every step, h ^ byte = h + ((s ^ byte)
+//    - s), so a chunk maps h to h * P^(4 n) + B (n logits). Pass 3 runs every
+//    chunk once from h = its starting low byte s, giving B = h_end - s P^(4n);
+//    the (P^(4n), B) pairs compose in order, h <- h A + B.
+// A bf16 logit widens to f32 bits w << 16: its bytes are 0, 0, lo, hi.
+constexpr uint32_t kP16 = (uint32_t)(kFnvPrime & 0xFFFF);
+constexpr uint32_t kP16sq = (uint32_t)((kFnvPrime * kFnvPrime) & 0xFFFF);
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t k) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * (u16x2){(uint16_t)k, (uint16_t)k});
+}
+
+// Passes 1 and 2: 16 runs of the low-byte chain over chunk k, two per
+// register (16-bit halves; the low byte of a product depends only on the
+// operands' low bytes, so the high bytes may hold anything). PASS 0 starts
+// run i at nibble i and records the final low nibbles; PASS 1 starts run i
+// at (i << 4) | low nibble of the chunk and records the final high nibbles.
+// maps[k] nibble i = the final nibble of run i.
+template <int PASS>
+__global__ void __launch_bounds__(256) hash_nibble_kernel(const uint16_t* logits, int64_t ld, int64_t chunks, int V,
+                                                          const uint8_t* __restrict__ start_lo,
+                                                          uint64_t* __restrict__ maps) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= chunks) return;
+  const uint32_t base = PASS == 0 ? 0u : start_lo[k];
+  uint32_t st[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t a = PASS == 0 ? 2 * i : (base | ((2 * i) << 4)), b = PASS == 0 ? 2 * i + 1 : (base | ((2 * i + 1) << 4));
+    st[i] = a | (b << 16);
+  }
+  int v0, v1;
+  chunk_range(V, (int)(k & (kEvalChunks - 1)), v0, v1);
+  walk_chunk(logits + (k / kEvalChunks) * ld, v0, v1, [&](uint32_t w) {
+    const uint32_t lo = (w & 0xFFu) * 0x10001u, hi = (w >> 8) * 0x10001u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st[i] = pk_mul(pk_mul(pk_mul(st[i], kP16sq) ^ lo, kP16) ^ hi, kP16);
+  });
+  uint64_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint32_t v = (st[i] >> (16 * hh)) & 0xFFu;
+      m |= (uint64_t)(PASS == 0 ? (v & 15u) : (v >> 4)) << (4 * (2 * i + hh));
+    }
+  maps[k] = m;
+}
+
+// 16-nibble maps: apply, and compose (first f, then g).
+__device__ __forceinline__ uint32_t nib_apply(uint64_t f, uint32_t s) { return (uint32_t)(f >> (4 * s)) & 15u; }
+__device__ __forceinline__ uint64_t nib_compose(uint64_t f, uint64_t g) {
+  uint64_t h = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) h |= (uint64_t)nib_apply(g, nib_apply(f, i)) << (4 * i);
+  return h;
+}
+constexpr uint64_t kNibIdentity = 0xFEDCBA9876543210ull;
+constexpr int kScanPer = 4, kScanBlock = 256 * kScanPer;  // chunks per scan workgroup
+
+// Ordered scan of the chunk maps, step 1: each workgroup's composition of
+// its kScanBlock maps (in order, by an order-preserving tree in LDS).
+__global__ void __launch_bounds__(256) nib_scan_up_kernel(const uint64_t* __restrict__ maps, int64_t chunks,
+                                                          uint64_t* __restrict__ agg) {
+  __shared__ uint64_t s[256];
+  const int t = threadIdx.x;
+  uint64_t f = kNibIdentity;
+  for (int i = 0; i < kScanPer; ++i) {
+    const int64_t k = (int64_t)blockIdx.x * kScanBlock + t * kScanPer + i;
+    if (k < chunks) f = nib_compose(f, maps[k]);
+  }
+  s[t] = f;
+  __syncthreads();
+  for (int w = 1; w < 256; w *= 2) {
+    if ((t & (2 * w - 1)) == 0) s[t] = nib_compose(s[t], s[t + w]);
+    __syncthreads();
+  }
+  if (t == 0) agg[blockIdx.x] = s[0];
+}
+
+// Step 2: the starting nibble of every workgroup, in order from `start`.
+__global__ void __launch_bounds__(64) nib_scan_top_kernel(const uint64_t* __restrict__ agg, int64_t nblocks,
+                                                          uint32_t start, uint8_t* __restrict__ bstart) {
+  if (threadIdx.x != 0) return;
+  uint32_t s = start;
+  for (int64_t b = 0; b < nblocks; ++b) {
+    bstart[b] = (uint8_t)s;
+    s = nib_apply(agg[b], s);
+  }
+}
+
+// Step 3: every chunk's starting nibble. OR_SHIFT 0 writes it to out[k];
+// 4 ORs it in as the high nibble (out then holds whole starting bytes).
+template <int OR_SHIFT>
+__global__ void __launch_bounds__(256) nib_scan_down_kernel(const uint64_t* __restrict__ maps, int64_t chunks,
+                                                            const uint8_t* __restrict__ bstart,
+                                                            uint8_t* __restrict__ out) {
+  __shared__ uint64_t s[256];
+  __shared__ uint8_t ts[256];
+  const int t = threadIdx.x;
+  uint64_t f = kNibIdentity;
+  for (int i = 0; i < kScanPer; ++i) {
+    const int64_t k = (int64_t)blockIdx.x * kScanBlock + t * kScanPer + i;
+    if (k < chunks) f = nib_compose(f, maps[k]);
+  }
+  s[t] = f;
+  __syncthreads();
+  if (t == 0) {
+    uint32_t st = bstart[blockIdx.x];
+    for (int i = 0; i < 256; ++i) {
+      ts[i] = (uint8_t)st;
+      st = nib_apply(s[i], st);
+    }
+  }
+  __syncthreads();
+  uint32_t st = ts[t];
+  for (int i = 0; i < kScanPer; ++i) {
+    const int64_t k = (int64_t)blockIdx.x * kScanBlock + t * kScanPer + i;
+    if (k >= chunks) break;
+    if (OR_SHIFT == 0) out[k] = (uint8_t)st;
+    else out[k] = (uint8_t)(out[k] | (st << 4));
+    st = nib_apply(maps[k], st);
+  }
+}
+
+// h * P mod 2^64 with P = 2^40 + 0x1B3.
+__device__ __forceinline__ uint64_t fnv_mul(uint64_t h) { return (h << 40) + h * 0x1B3ull; }
+
+struct Affine {
+  uint64_t a, b;  // h -> h * a + b
+};
+// first x, then y
+__device__ __forceinline__ Affine affine_then(Affine x, Affine y) { return Affine{x.a * y.a, x.b * y.a + y.b}; }
+
+// Pass 3: each chunk run once from h = its starting low byte, reduced to one
+// affine map per workgroup of 256 chunks (order-preserving tree).
+__global__ void __launch_bounds__(256) hash_affine_kernel(const uint16_t* logits, int64_t ld, int64_t chunks, int V,
+                                                          const uint8_t* __restrict__ start_byte,
+                                                          Affine* __restrict__ out) {
+  __shared__ uint64_t sa[256], sb[256];
+  const int t = threadIdx.x;
+  const int64_t k = (int64_t)blockIdx.x * 256 + t;
+  Affine f{1, 0};
+  if (k < chunks) {
+    int v0, v1;
+    chunk_range(V, (int)(k & (kEvalChunks - 1)), v0, v1);
+    const uint64_t s0 = start_byte[k];
+    uint64_t h = s0;
+    walk_chunk(logits + (k / kEvalChunks) * ld, v0, v1, [&](uint32_t w) {
+      h = fnv_mul(fnv_mul(h));
+      h = fnv_mul(h ^ (w & 0xFFu));
+      h = fnv_mul(h ^ (w >> 8));
+    });
+    // P^(4 n) by squaring
+    uint64_t a = 1, p4 = fnv_mul(fnv_mul(fnv_mul(kFnvPrime)));
+    for (uint32_t n = (uint32_t)(v1 - v0); n; n >>= 1, p4 *= p4)
+      if (n & 1) a *= p4;
+    f = Affine{a, h - s0 * a};
+  }
+  sa[t] = f.a;
+  sb[t] = f.b;
+  __syncthreads();
+  for (int w = 1; w < 256; w *= 2) {
+    if ((t & (2 * w - 1)) == 0) {
+      const Affine r = affine_then(Affine{sa[t], sb[t]}, Affine{sa[t + w], sb[t + w]});
+      sa[t] = r.a;
+      sb[t] = r.b;
+    }
+    __syncthreads();
+  }
+  if (t == 0) out[blockIdx.x] = Affine{sa[0], sb[0]};
 }
 
 struct ModelWs {
@@ -505,29 +711,110 @@ glt_status glt_model_fwd(const glt_model* m, const int32_t* ids, uint16_t* logit
   return glt_lm_head_fwd(x_ffn, (int32_t)M, D, m->lm_head, m->lm_head_prepared, m->V, logits, stream);
 }
 
+}  // extern "C"
+
+namespace glt {
+namespace {
+struct EvalWs {
+  size_t rows, maps, start, agg, bstart, aff, total;
+  int64_t chunks, nscan, naff;
+};
+EvalWs eval_ws(int64_t R) {
+  EvalWs w{};
+  w.chunks = R * kEvalChunks;
+  w.nscan = cdiv(w.chunks, kScanBlock);
+  w.naff = cdiv(w.chunks, 256);
+  w.rows = 0;
+  w.maps = up(w.rows + R * sizeof(EvalRow));
+  w.start = up(w.maps + w.chunks * 8);
+  w.agg = up(w.start + w.chunks);
+  w.bstart = up(w.agg + w.nscan * 8);
+  w.aff = up(w.bstart + w.nscan);
+  w.total = up(w.aff + w.naff * sizeof(Affine));
+  return w;
+}
+
+// Starting nibble of every chunk from the maps (ordered scan, three launches).
+glt_status nib_scan(const EvalWs& w, char* ws, uint32_t start, bool high, hipStream_t st) {
+  const uint64_t* maps = reinterpret_cast<const uint64_t*>(ws + w.maps);
+  uint64_t* agg = reinterpret_cast<uint64_t*>(ws + w.agg);
+  uint8_t* bstart = reinterpret_cast<uint8_t*>(ws + w.bstart);
+  uint8_t* out = reinterpret_cast<uint8_t*>(ws + w.start);
+  GLT_LAUNCH("eval_hash_scan", nib_scan_up_kernel, dim3((unsigned)w.nscan), dim3(256), 0, st, maps, w.chunks, agg);
+  GLT_LAUNCH_CHECK("nib_scan_up");
+  GLT_LAUNCH("eval_hash_scan", nib_scan_top_kernel, dim3(1), dim3(64), 0, st, agg, w.nscan, start, bstart);
+  GLT_LAUNCH_CHECK("nib_scan_top");
+  if (high)
+    GLT_LAUNCH("eval_hash_scan", nib_scan_down_kernel<4>, dim3((unsigned)w.nscan), dim3(256), 0, st, maps, w.chunks,
+               bstart, out);
+  else
+    GLT_LAUNCH("eval_hash_scan", nib_scan_down_kernel<0>, dim3((unsigned)w.nscan), dim3(256), 0, st, maps, w.chunks,
+               bstart, out);
+  GLT_LAUNCH_CHECK("nib_scan_down");
+  return GLT_OK;
+}
+}  // namespace
+}  // namespace glt
+
+extern "C" {
+
 size_t glt_eval_stats_workspace_size(int32_t B, int32_t T) {
-  return (B > 0 && T > 0) ? up((size_t)B * T * sizeof(EvalRow)) : 256;
+  return (B > 0 && T > 0) ? eval_ws((int64_t)B * T).total : 256;
 }
 
 glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids, int32_t B, int32_t T, int32_t V,
-                          glt_eval_result* out, void* workspace, size_t workspace_bytes, void* stream) {
+                          int32_t hash_mode, uint64_t hash_in, glt_eval_result* out, void* workspace,
+                          size_t workspace_bytes, void* stream) {
   GLT_CHECK(out && B >= 0 && T >= 0 && V > 0 && ld >= V, GLT_ERR_SHAPE, "glt_eval_stats: B=%d T=%d V=%d", B, T, V);
-  *out = glt_eval_result{0.0, 0, 0.0, 0.0, kFnvBasis};
+  GLT_CHECK(hash_mode == GLT_EVAL_HASH_REFERENCE || hash_mode == GLT_EVAL_HASH_ROWS, GLT_ERR_INVALID_ARG,
+            "glt_eval_stats: hash_mode %d", hash_mode);
+  *out = glt_eval_result{0.0, 0, 0.0, 0.0, hash_in};
   const int64_t R = (int64_t)B * T;
   if (R == 0) return GLT_OK;
   GLT_CHECK(logits && ids, GLT_ERR_INVALID_ARG, "glt_eval_stats: null logits/ids");
-  GLT_CHECK(workspace && workspace_bytes >= glt_eval_stats_workspace_size(B, T), GLT_ERR_WORKSPACE,
-            "glt_eval_stats: needs %zu workspace bytes", glt_eval_stats_workspace_size(B, T));
+  GLT_CHECK(workspace && workspace_bytes >= glt_eval_stats_workspace_size(B, T) &&
+                reinterpret_cast<uintptr_t>(workspace) % kAlign == 0,
+            GLT_ERR_WORKSPACE, "glt_eval_stats: needs %zu workspace bytes, %zu-byte aligned",
+            glt_eval_stats_workspace_size(B, T), kAlign);
+  const bool exact = hash_mode == GLT_EVAL_HASH_REFERENCE;
+  const EvalWs w = eval_ws(R);
+  GLT_CHECK(w.naff < INT32_MAX, GLT_ERR_SHAPE, "glt_eval_stats: %lld rows", (long long)R);
   hipStream_t st = as_stream(stream);
-  EvalRow* rows = static_cast<EvalRow*>(workspace);
-  GLT_LAUNCH("eval_rows", eval_rows_kernel, dim3((unsigned)((R + 15) / 16)), dim3(256), 0, st, logits, ld, ids, B, T,
-             V, rows);
+  char* ws = static_cast<char*>(workspace);
+  EvalRow* rows = reinterpret_cast<EvalRow*>(ws + w.rows);
+  if (exact)
+    GLT_LAUNCH("eval_rows", eval_rows_kernel<false>, dim3((unsigned)((R + 15) / 16)), dim3(256), 0, st, logits, ld,
+               ids, B, T, V, rows);
+  else
+    GLT_LAUNCH("eval_rows", eval_rows_kernel<true>, dim3((unsigned)((R + 15) / 16)), dim3(256), 0, st, logits, ld,
+               ids, B, T, V, rows);
   GLT_LAUNCH_CHECK("eval_rows");
+  Affine* aff = reinterpret_cast<Affine*>(ws + w.aff);
+  if (exact) {
+    uint64_t* maps = reinterpret_cast<uint64_t*>(ws + w.maps);
+    uint8_t* start = reinterpret_cast<uint8_t*>(ws + w.start);
+    const dim3 grid((unsigned)w.naff);
+    GLT_LAUNCH("eval_hash_nibble", hash_nibble_kernel<0>, grid, dim3(256), 0, st, logits, ld, w.chunks, V,
+               (const uint8_t*)nullptr, maps);
+    GLT_LAUNCH_CHECK("hash_nibble");
+    glt_status s = nib_scan(w, ws, (uint32_t)(hash_in & 15), false, st);
+    if (s != GLT_OK) return s;
+    GLT_LAUNCH("eval_hash_nibble", hash_nibble_kernel<1>, grid, dim3(256), 0, st, logits, ld, w.chunks, V,
+               (const uint8_t*)start, maps);
+    GLT_LAUNCH_CHECK("hash_nibble");
+    if ((s = nib_scan(w, ws, (uint32_t)((hash_in >> 4) & 15), true, st)) != GLT_OK) return s;
+    GLT_LAUNCH("eval_hash_affine", hash_affine_kernel, grid, dim3(256), 0, st, logits, ld, w.chunks, V,
+               (const uint8_t*)start, aff);
+    GLT_LAUNCH_CHECK("hash_affine");
+  }
   std::vector<EvalRow> h((size_t)R);
+  std::vector<Affine> ha(exact ? (size_t)w.naff : 0);
   GLT_CHECK(hipMemcpyAsync(h.data(), rows, (size_t)R * sizeof(EvalRow), hipMemcpyDeviceToHost, st) == hipSuccess &&
+                (!exact || hipMemcpyAsync(ha.data(), aff, ha.size() * sizeof(Affine), hipMemcpyDeviceToHost, st) ==
+                               hipSuccess) &&
                 hipStreamSynchronize(st) == hipSuccess,
-            GLT_ERR_HIP, "glt_eval_stats: copy of the row results failed");
-  uint64_t hash = kFnvBasis;
+            GLT_ERR_HIP, "glt_eval_stats: copy of the results failed");
+  uint64_t hash = hash_in;
   for (const EvalRow& r : h) {
     out->logits_sum += r.sum;
     out->logits_sumsq += r.sumsq;
@@ -535,11 +822,13 @@ glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids
       out->total_nll += r.nll;
       ++out->count;
     }
-    for (int k = 0; k < 8; ++k) {
-      hash ^= (r.hash >> (8 * k)) & 0xFFu;
-      hash *= kFnvPrime;
-    }
+    if (!exact)
+      for (int k = 0; k < 8; ++k) {
+        hash ^= (r.hash >> (8 * k)) & 0xFFu;
+        hash *= kFnvPrime;
+      }
   }
+  for (const Affine& a : ha) hash = hash * a.a + a.b;
   out->logits_hash = hash;
   return GLT_OK;
 }

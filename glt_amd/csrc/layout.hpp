@@ -70,6 +70,9 @@ glt_status shuffle_b_tr_pair(const void* src0, const void* src1, int src_dtype, 
 glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed, int rows, int K, uint16_t* dst,
                      hipStream_t st);
 
+// out[i] = RNE bf16 of in[i].
+glt_status convert_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st);
+
 // Packed-mirror orientations q = 2*proj and 2*proj+1 (row-major and
 // shuffled) of one projection from its f32 [S,H] master.
 glt_status pack_projection(const float* master, int S, int H, int proj, uint16_t* packed, hipStream_t st);

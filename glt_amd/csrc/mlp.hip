@@ -154,8 +154,8 @@ static glt_status down_forward(const glt_mlp_desc* d, const glt_base_weights* w,
 }
 
 struct BwdLayout {
-  size_t dg, du, xt, dyt, g, u, inter, slice0, slice_stride, total;
-  bool wgrad_mfma;
+  size_t dg, du, dyb, xt, dyt, g, u, inter, slice0, slice_stride, total;
+  bool wgrad_mfma, dy_f32;
 };
 
 // The weight gradients reduce over the M tokens; on the MFMA kernel that K
@@ -170,6 +170,12 @@ static BwdLayout bwd_layout(const glt_mlp_desc* d) {
   size_t off = 0;
   L.dg = off; off += align256(MN);
   L.du = off; off += align256(MN);
+  // an f32 upstream gradient on the bf16 path is rounded once into here
+  L.dy_f32 = (d->flags & GLT_MLP_DY_F32) && d->dtype == GLT_DTYPE_BF16;
+  if (L.dy_f32) {
+    L.dyb = off;
+    off += align256((size_t)d->M * d->D * 2);
+  }
   if (d->flags & GLT_MLP_RECOMPUTE) {
     L.g = off; off += align256(MN);
     L.u = off; off += align256(MN);
@@ -267,6 +273,17 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
   const int M = d->M, D = d->D, I = d->I, N = d->N;
   void* dg = W + L.dg;
   void* du = W + L.du;
+
+  if (L.dy_f32) {
+    // The reference multiplies its f32 upstream gradient by the f32 copy of
+    // W_down (src/layer_backward_impl.inc:48) and rounds it to bf16 for the
+    // graft GEMMs (src/gemm_impl.inc:454-455, :524-525). The MFMA operands
+    // are bf16, so the gradient is rounded once (RNE) here and every GEMM
+    // below reads that copy.
+    uint16_t* dyb = reinterpret_cast<uint16_t*>(W + L.dyb);
+    if ((s = convert_f32_to_bf16(static_cast<const float*>(dy), dyb, (int64_t)d->M * d->D, st)) != GLT_OK) return s;
+    dy = dyb;
+  }
 
   if (recompute) {
     gate_pre = W + L.g;

@@ -99,10 +99,10 @@ class BaseMLP:
         return F.BaseWeights(_p(self.gate), _p(self.up), _p(self.down), _p(self.prepared))
 
 
-def _desc(base, slices, M, N, explicit, recompute=False, state=None, residual=False):
+def _desc(base, slices, M, N, explicit, recompute=False, state=None, residual=False, dy_f32=False):
     arr = _slices_array(slices)
     flags = ((F.MLP_EXPLICIT if explicit else 0) | (F.MLP_RECOMPUTE if recompute else 0)
-             | (F.MLP_RESIDUAL if residual else 0))
+             | (F.MLP_RESIDUAL if residual else 0) | (F.MLP_DY_F32 if dy_f32 else 0))
     d = F.MlpDesc(M, base.D, base.I, N, _dtype_code(base.dtype), flags, len(slices), arr,
                   ctypes.pointer(state) if state is not None else None)
     return d, arr
@@ -133,10 +133,12 @@ def mlp_backward_workspace(base, slices, M, N, explicit=True, recompute=False):
 def mlp_backward(base, slices, x, dy, N, gate_pre=None, up_pre=None, inter=None, want_dx=True, explicit=True,
                  recompute=False, state=None, workspace=None):
     """Graft-only backward (reference backward_layer FFN section,
-    src/layer_backward_impl.inc:10-361). Returns dx (f32) and per-slice
-    [gate, up, down] f32 gradients in [S,H] storage."""
+    src/layer_backward_impl.inc:10-361). dy is [M,D] in the path dtype or
+    f32 (the reference's upstream gradient, rounded once inside on the bf16
+    path). Returns dx (f32) and per-slice [gate, up, down] f32 gradients in
+    [S,H] storage."""
     M = x.shape[0]
-    d, keep = _desc(base, slices, M, N, explicit, recompute, state)
+    d, keep = _desc(base, slices, M, N, explicit, recompute, state, dy_f32=dy.dtype == torch.float32)
     nbytes = F.load().glt_mlp_bwd_workspace_size(ctypes.byref(d))
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
@@ -211,14 +213,19 @@ def adamw_step(w, g, m, v, step, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_de
 
 
 def adamw_graft_step(slices, grads, m, v, step, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
-                     proj_mask=7):
-    """AdamW over graft slices with the packed-mirror refresh fused in.
+                     proj_mask=7, clip_norm=0.0, workspace=None):
+    """AdamW over graft slices with the packed-mirror refresh fused in and
+    the optional global-L2 clip over all of their gradients (reference
+    grafting.hip:1149-1164, clip 1.0 by default there).
     grads/m/v: per slice a flat f32 [3*S*H] tensor (gate, up, down)."""
     arr = _slices_array(slices)
+    nbytes = F.load().glt_adamw_workspace_size(0)
+    if clip_norm > 0 and workspace is None:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=grads[0].device)
     F.call("glt_adamw_graft_step", arr, len(slices), F.ptr_array([g.data_ptr() for g in grads]),
            F.ptr_array([t.data_ptr() for t in m]), F.ptr_array([t.data_ptr() for t in v]),
            F.ptr_array([s.packed.data_ptr() for s in slices]), proj_mask, step, lr, beta1, beta2, eps,
-           weight_decay, _stream())
+           weight_decay, clip_norm, _p(workspace), nbytes if workspace is not None else 0, _stream())
 
 
 def shadow_bake(state, gate, up, down, grafts, placements, *, D, I, N=None, materialize=False, gate_out=None,
@@ -508,18 +515,41 @@ def embedding(ids, table):
     return out
 
 
-def eval_stats(logits, ids):
+def eval_stats(logits, ids, hash_in=F.FNV_BASIS, reference_hash=True):
     """Shadow-eval terms of one batch (reference grafting.hip:504-547):
-    dict(total_nll, count, ce, logits_sum, logits_sumsq, logits_hash)."""
+    dict(total_nll, count, ce, logits_sum, logits_sumsq, logits_hash).
+    The hash is the reference's FNV-1a chain over every f32 logit byte,
+    continued from hash_in (pass the previous batch's logits_hash to chain
+    batches as the reference does); reference_hash=False gives the library's
+    one-pass row form instead."""
     B, T = ids.shape
     V = logits.shape[-1]
+    assert logits.stride(-1) == 1, "logits rows must be contiguous"
+    ld = logits.stride(-2)
     lib = F.load()
     nbytes = lib.glt_eval_stats_workspace_size(B, T)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
     r = F.EvalResult()
-    F.call("glt_eval_stats", _p(logits), V, _p(ids), B, T, V, ctypes.byref(r), _p(ws), nbytes, _stream())
+    F.call("glt_eval_stats", _p(logits), ld, _p(ids), B, T, V,
+           F.EVAL_HASH_REFERENCE if reference_hash else F.EVAL_HASH_ROWS, hash_in, ctypes.byref(r), _p(ws), nbytes,
+           _stream())
     return {"total_nll": r.total_nll, "count": r.count, "ce": r.total_nll / max(r.count, 1),
             "logits_sum": r.logits_sum, "logits_sumsq": r.logits_sumsq, "logits_hash": r.logits_hash}
+
+
+def eval_batches(batches, reference_hash=True):
+    """The reference's whole eval loop over several (logits, ids) batches
+    (grafting.hip:504-547): nll and counts summed, the logits hash chained
+    from the FNV basis through every batch; returns the eval_stats dict of
+    the whole set (ce = total_nll / count)."""
+    out = {"total_nll": 0.0, "count": 0, "logits_sum": 0.0, "logits_sumsq": 0.0, "logits_hash": F.FNV_BASIS}
+    for logits, ids in batches:
+        r = eval_stats(logits, ids, out["logits_hash"], reference_hash)
+        for k in ("total_nll", "count", "logits_sum", "logits_sumsq"):
+            out[k] += r[k]
+        out["logits_hash"] = r["logits_hash"]
+    out["ce"] = out["total_nll"] / max(out["count"], 1)
+    return out
 
 
 def certify(A, B, C, D, ce_improve_margin=0.0, eps_ce_bake=0.02, eps_ce_reload=1e-4):

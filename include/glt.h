@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GLT_ABI_VERSION 2
+#define GLT_ABI_VERSION 3
 
 /* ------------------------------------------------------------------ status */
 typedef int32_t glt_status;
@@ -126,6 +126,11 @@ typedef struct {
  * y = round(y + round(ffn_out)) (the reference's x = x + ffn_out,
  * src/layer_forward_impl.inc:271-275, on the path dtype). */
 #define GLT_MLP_RESIDUAL 4
+/* GLT_MLP_DY_F32: glt_mlp_bwd's dy is f32 [M,D] on the bf16 path (the
+ * reference's backward receives an f32 gradient, src/layer_backward_impl.inc:48).
+ * It is rounded once (RNE) to the bf16 MFMA operand inside the call; without
+ * the flag dy is in the path dtype. No effect on the f32 path (dy is f32). */
+#define GLT_MLP_DY_F32 8
 typedef struct {
   int32_t M, D, I, N;
   int32_t dtype;   /* GLT_DTYPE_BF16 or GLT_DTYPE_F32 */
@@ -226,7 +231,7 @@ glt_status glt_mlp_fwd(const glt_mlp_desc* d, const glt_base_weights* w,
  * src/layer_backward_impl.inc:10-361; base weights frozen):
  *   dInter = dy . W_down_ext ; dgate/dup via the SiLU*up derivative;
  *   grads[j] = per-slice dW (f32, [S,H] storage); dx = d(x) f32 [M,D].
- * dy is [M,D] of the path dtype. dx nullable. Returns
+ * dy is [M,D] of the path dtype, or f32 with GLT_MLP_DY_F32. dx nullable. Returns
  * GLT_ERR_BAKED_NO_BACKWARD when d->state says the model is shadow-baked
  * (reference src/layer_backward_impl.inc:11-13). */
 size_t glt_mlp_bwd_workspace_size(const glt_mlp_desc* d);
@@ -368,7 +373,9 @@ glt_status glt_grft_load_raw_f32(const char* path, const glt_grft_info* expect, 
  * global L2 norm <= clip_norm using sqrt(sum g^2 + 1e-8) (reference
  * reduce_l2/calc_scale/apply_scale, src/kernels_elementwise_impl.inc:133-213);
  * clip_norm <= 0 = no clip. The clip needs ws of glt_adamw_workspace_size(n)
- * bytes. bf16_mirror (nullable) receives bf16(w). */
+ * bytes. bf16_mirror (nullable) receives bf16(w). g is read only (the
+ * reference scales its gradient buffer in place; here the scale is applied
+ * as the update reads it). */
 size_t glt_adamw_workspace_size(int64_t n);
 glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* bf16_mirror,
                           int64_t n, int32_t step, float lr, float beta1, float beta2,
@@ -379,12 +386,18 @@ glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* bf16
  * updates each slice's masters (treated as writable) and rewrites the
  * updated projections' part of its packed bf16 mirror. grads/m/v are per-slice [3,S,H]
  * f32 buffers laid out gate,up,down. proj_mask as in the reference
- * (skipped projections are untouched, src/kernels_optimizer_impl.inc:20-25). */
+ * (skipped projections are untouched, src/kernels_optimizer_impl.inc:20-25).
+ * clip_norm > 0 clips first by the global L2 norm over the gradients of every
+ * projection the step updates, all slices together (the reference's
+ * per-step clip over all of its deltas, grafting.hip:1149-1164, default
+ * 1.0, src/config.hpp:85); it needs ws of glt_adamw_workspace_size(0)
+ * bytes. At most 8 slices per call. */
 glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
                                 float* const* grads, float* const* m, float* const* v,
                                 uint16_t* const* packed_out, int32_t proj_mask,
                                 int32_t step, float lr, float beta1, float beta2,
-                                float eps, float weight_decay, void* stream);
+                                float eps, float weight_decay, float clip_norm, void* ws,
+                                size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------ shadow bake */
 /* Merge graft deltas into bf16 base matrices (reference shadow_bake_kernel /
@@ -411,7 +424,7 @@ typedef struct {
   int32_t proj_mask;
   int32_t D, I, N;                /* N used by MATERIALIZE (N >= I) */
   int32_t graft_dtype;            /* GLT_DTYPE_F32 (master) or GLT_DTYPE_BF16 */
-  int32_t n_slices;               /* slices baked together (stacked grafts) */
+  int32_t n_slices;               /* slices baked together (stacked grafts), at most 8 */
   const int32_t* placement;       /* n_slices x {i_start, s, h_start, h} */
   const void* const* graft;       /* [n_slices * num_layers] flat [3,S,H] per layer */
 } glt_bake_desc;
@@ -462,14 +475,27 @@ glt_status glt_model_fwd(const glt_model* m, const int32_t* ids, uint16_t* logit
  * grafting.hip:504-547): over rows (b,t) of B*T bf16 logits (row stride
  * ld), the f32 cross-entropy of rows t < T-1 against ids[b,t+1] summed in
  * f64 (total_nll; mean = total_nll / count), the f64 sum and sum of squares
- * of every logit, and a 64-bit FNV-1a hash: each row's f32 logits cut into
- * 16 chunks of ceil(V/16) (the last ones shorter or empty), each chunk
- * hashed byte by byte (little-endian) from the FNV offset basis, the chunk
- * hashes' 8 bytes hashed in chunk order into the row hash, and the row
- * hashes' 8 bytes chained in row order. (The reference chains every byte of
- * the batch in one sequence; this form is computed in parallel, so the value
- * differs while serving the same purpose: equal logits give equal hashes.)
- * Synchronous; workspace: glt_eval_stats_workspace_size bytes. */
+ * of every logit, and a 64-bit FNV-1a hash of the logits.
+ *
+ * hash_mode GLT_EVAL_HASH_REFERENCE: the reference's hash, bit for bit: one
+ * FNV-1a chain, h = (h ^ byte) * 1099511628211 mod 2^64, over the four
+ * little-endian bytes of every f32 logit in (b, t, v) order, starting from
+ * hash_in (grafting.hip:536-546). The reference starts at GLT_FNV_BASIS and
+ * continues the chain across its eval batches: pass the previous batch's
+ * logits_hash as hash_in to do the same. Computed exactly in parallel (the
+ * low byte of the state is a chain of its own, after which each chunk of
+ * logits is an affine map mod 2^64).
+ * hash_mode GLT_EVAL_HASH_ROWS: this library's row form: each row's f32
+ * logits cut into 16 chunks of ceil(V/16) (the last ones shorter or empty),
+ * each chunk hashed byte by byte from GLT_FNV_BASIS, the chunk hashes' 8
+ * bytes hashed in chunk order into the row hash, and the row hashes' 8 bytes
+ * chained in row order from hash_in (one pass over the logits; a different
+ * value from the reference's).
+ * Synchronous; workspace: glt_eval_stats_workspace_size bytes, 256-byte
+ * aligned. */
+#define GLT_FNV_BASIS 1469598103934665603ULL /* the reference's offset basis, grafting.hip:505 */
+#define GLT_EVAL_HASH_REFERENCE 0
+#define GLT_EVAL_HASH_ROWS      1
 typedef struct {
   double total_nll;
   int64_t count;
@@ -478,8 +504,8 @@ typedef struct {
 } glt_eval_result;
 size_t glt_eval_stats_workspace_size(int32_t B, int32_t T);
 glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids, int32_t B, int32_t T,
-                          int32_t V, glt_eval_result* out, void* workspace, size_t workspace_bytes,
-                          void* stream);
+                          int32_t V, int32_t hash_mode, uint64_t hash_in, glt_eval_result* out,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------ base model files
  * Safetensors model weights (reference load_base_model_safetensors /

@@ -250,9 +250,9 @@ typedef struct {
  *   for each slice: y[:, h-slice] = bf16(y + inter[:, i-slice] . bf16(Dd))   (:186-218)
  * Base rows [I,N) are zero (appended neurons). bf16 = 0 gives the f32 path
  * (no roundings). x [M,D], wg/wu [I,D], wd [D,I]; outputs [M,N] / [M,D]. */
-void orc_mlp_fwd(int M, int D, int I, int N, int bf16, int n_slices, const orc_slice* sl, const float* x,
-                 const float* wg, const float* wu, const float* wd, float* gate_pre, float* up_pre, float* inter,
-                 float* y) {
+void orc_mlp_fwd_mode(int M, int D, int I, int N, int bf16, int recompute, int n_slices, const orc_slice* sl,
+                      const float* x, const float* wg, const float* wu, const float* wd, float* gate_pre,
+                      float* up_pre, float* inter, float* y) {
   const int64_t MN = (int64_t)M * N;
   float* tmp = (float*)malloc(sizeof(float) * (size_t)M * (N > D ? N : D));
   float* dbf = NULL;
@@ -275,12 +275,21 @@ void orc_mlp_fwd(int M, int D, int I, int N, int bf16, int n_slices, const orc_s
       for (int m = 0; m < M; ++m)
         for (int c = 0; c < s->s; ++c) {
           float* o = out + (int64_t)m * N + s->i0 + c;
-          const float r = *o + tmp[(int64_t)m * s->s + c];
+          /* forward: the f32 delta joins the bf16 base, one rounding;
+           * recompute: the cached delta is cast to bf16 first and added in
+           * bf16 (gate_slice.add_(delta.to(bf16))) */
+          const float dv = tmp[(int64_t)m * s->s + c];
+          const float r = *o + ((bf16 && recompute) ? rb(dv) : dv);
           *o = bf16 ? rb(r) : r;
         }
     }
   }
   orc_silu_mul(gate_pre, up_pre, inter, MN, bf16);
+  if (!y) {
+    free(dbf);
+    free(tmp);
+    return;
+  }
   memset(y, 0, sizeof(float) * (size_t)M * D);
   if (I > 0) {
     gemm_nt(M, D, I, inter, N, wd, I, tmp, D);
@@ -302,6 +311,33 @@ void orc_mlp_fwd(int M, int D, int I, int N, int bf16, int n_slices, const orc_s
   }
   free(dbf);
   free(tmp);
+}
+
+void orc_mlp_fwd(int M, int D, int I, int N, int bf16, int n_slices, const orc_slice* sl, const float* x,
+                 const float* wg, const float* wu, const float* wd, float* gate_pre, float* up_pre, float* inter,
+                 float* y) {
+  orc_mlp_fwd_mode(M, D, I, N, bf16, 0, n_slices, sl, x, wg, wu, wd, gate_pre, up_pre, inter, y);
+}
+
+/* The reference's recompute_ffn (src/layer_recompute_impl.inc:8-91): gate and
+ * up from at::linear in bf16 (:20, :46), each slice's cached expand output
+ * (the forward's f32 delta, acts.delta_gate_out) cast to bf16 and added into
+ * the bf16 slice in place (:33-38, :59-64), i.e. bf16(bf16(base) +
+ * bf16(delta)) where the forward rounds once, bf16(bf16(base) + delta)
+ * (src/kernels_elementwise_impl.inc:314-326); inter = silu(gate)*up (:66-82). */
+void orc_mlp_recompute(int M, int D, int I, int N, int n_slices, const orc_slice* sl, const float* x,
+                       const float* wg, const float* wu, float* gate_pre, float* up_pre, float* inter) {
+  orc_mlp_fwd_mode(M, D, I, N, 1, 1, n_slices, sl, x, wg, wu, NULL, gate_pre, up_pre, inter, NULL);
+}
+
+/* 64-bit FNV-1a over n bytes from h (the reference's logits hash step,
+ * grafting.hip:536-546: h ^= byte; h *= 1099511628211). */
+uint64_t orc_fnv1a64(const uint8_t* p, int64_t n, uint64_t h) {
+  for (int64_t i = 0; i < n; ++i) {
+    h ^= p[i];
+    h *= 1099511628211ULL;
+  }
+  return h;
 }
 
 /* Graft-only backward of the reference (src/layer_backward_impl.inc:34-361)

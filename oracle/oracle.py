@@ -63,6 +63,9 @@ def _setup(L):
     L.orc_silu_mul.argtypes = [_f, _f, _f, _i64, _i]
     L.orc_gate_up_bwd.argtypes = [_f, _f, _f, _f, _f, _i64]
     L.orc_mlp_fwd.argtypes = [_i, _i, _i, _i, _i, _i, ctypes.POINTER(Slice), _f, _f, _f, _f, _f, _f, _f, _f]
+    L.orc_mlp_recompute.argtypes = [_i, _i, _i, _i, _i, ctypes.POINTER(Slice), _f, _f, _f, _f, _f, _f]
+    L.orc_fnv1a64.restype = ctypes.c_uint64
+    L.orc_fnv1a64.argtypes = [ctypes.c_void_p, _i64, ctypes.c_uint64]
     L.orc_mlp_bwd.argtypes = [_i, _i, _i, _i, _i, _i, ctypes.POINTER(Slice), _f, _f, _f, _f, _f, _f, _f, _f,
                               _f, ctypes.POINTER(_f)]
 
@@ -190,6 +193,28 @@ def attention(q, k, v, causal=True, scale=None):
     return out
 
 
+def attention_rows(q_rows, k, v, b_idx, t_idx, causal=True, scale=None):
+    """attention() for selected query positions only: q_rows [n,Hq,hd] are
+    the queries of positions (b_idx[i], t_idx[i]); k/v [B,T,Hkv,hd]. Same
+    float64 softmax; returns [n,Hq,hd] float64."""
+    n, Hq, hd = q_rows.shape
+    Hkv = k.shape[2]
+    rep = Hq // Hkv
+    scale = hd ** -0.5 if scale is None else scale
+    out = np.zeros((n, Hq, hd))
+    for i in range(n):
+        b, t = int(b_idx[i]), int(t_idx[i])
+        end = t + 1 if causal else k.shape[1]
+        for h in range(Hq):
+            g = h // rep
+            s = (np.asarray(k[b, :end, g], np.float64) @ np.asarray(q_rows[i, h], np.float64)) * scale
+            s -= s.max()
+            p = np.exp(s)
+            p /= p.sum()
+            out[i, h] = p @ np.asarray(v[b, :end, g], np.float64)
+    return out
+
+
 # ---------------------------------------------------------------- AdamW
 def adamw(w, g, m, v, step, lr, b1, b2, eps, wd, clip_norm=0.0):
     w, g, m, v = _c32(w).copy(), _c32(g), _c32(m).copy(), _c32(v).copy()
@@ -240,6 +265,21 @@ def mlp_fwd(x, wg, wu, wd, N, slices, bf16=True):
     lib().orc_mlp_fwd(M, D, I, N, int(bf16), len(slices), arr, _fp(x), _fp(wg), _fp(wu), _fp(wd), _fp(g), _fp(u),
                       _fp(inter), _fp(y))
     return g, u, inter, y
+
+
+def mlp_recompute(x, wg, wu, N, slices):
+    """The reference's recompute_ffn rounding (src/layer_recompute_impl.inc:8-91):
+    returns (gate_pre, up_pre, inter) with each slice's delta rounded to bf16
+    before it is added to the bf16 base pre-activation."""
+    x, wg, wu = _c32(x), _c32(wg), _c32(wu)
+    M, D = x.shape
+    I = wg.shape[0]
+    arr, keep = _slices(slices)
+    g = np.empty((M, N), np.float32)
+    u = np.empty((M, N), np.float32)
+    inter = np.empty((M, N), np.float32)
+    lib().orc_mlp_recompute(M, D, I, N, len(slices), arr, _fp(x), _fp(wg), _fp(wu), _fp(g), _fp(u), _fp(inter))
+    return g, u, inter
 
 
 def mlp_bwd(x, wg, wu, wd, N, slices, g, u, inter, dy, bf16=True, want_dx=True):
@@ -378,6 +418,20 @@ def fnv1a64(data, h=FNV_BASIS):
     return h
 
 
+def fnv1a64_c(data, h=FNV_BASIS):
+    """fnv1a64 through the C oracle (large inputs)."""
+    a = np.ascontiguousarray(np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray)
+                             else data.view(np.uint8).reshape(-1))
+    return int(lib().orc_fnv1a64(a.ctypes.data_as(ctypes.c_void_p), a.size, h))
+
+
+def eval_hash_reference(logits, h=FNV_BASIS):
+    """The reference's logits hash (grafting.hip:536-546): one FNV-1a chain
+    from h over the four little-endian bytes of every f32 logit, b, t, v in
+    order (logits [.., V] f32 holding the bf16 values)."""
+    return fnv1a64_c(np.ascontiguousarray(np.asarray(logits, np.float32).astype("<f4")), h)
+
+
 EVAL_CHUNKS = 16
 
 
@@ -394,18 +448,22 @@ def eval_row_hash(row):
     return h
 
 
-def eval_stats(logits, ids):
-    """Shadow-eval terms (reference grafting.hip:504-547) in the library's
-    parallel hash form: each row hashed by eval_row_hash, the row hashes'
-    little-endian bytes chained in row order; f64 NLL of rows t < T-1
-    against ids[b, t+1]; f64 sum and sum of squares."""
+def eval_stats(logits, ids, hash_in=FNV_BASIS, reference_hash=True):
+    """Shadow-eval terms (reference grafting.hip:504-547): the logits hash
+    continued from hash_in, either the reference's (eval_hash_reference) or
+    the library's row form (each row hashed by eval_row_hash, the row
+    hashes' little-endian bytes chained in row order); f64 NLL of rows
+    t < T-1 against ids[b, t+1]; f64 sum and sum of squares."""
     x = np.asarray(logits, np.float32)
     B, T = np.asarray(ids).shape
     V = x.shape[-1]
     rows = x.reshape(B * T, V)
-    h = FNV_BASIS
-    for r in rows:
-        h = fnv1a64(int(eval_row_hash(r)).to_bytes(8, "little"), h)
+    if reference_hash:
+        h = eval_hash_reference(rows, hash_in)
+    else:
+        h = hash_in
+        for r in rows:
+            h = fnv1a64(int(eval_row_hash(r)).to_bytes(8, "little"), h)
     r64 = rows.astype(np.float64)
     scored = r64.reshape(B, T, V)[:, :T - 1].reshape(-1, V)
     lab = np.asarray(ids)[:, 1:].reshape(-1)

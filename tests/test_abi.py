@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from glt_amd import _ffi
     lib = _ffi.load()
-    assert lib.glt_version() == 2
+    assert lib.glt_version() == 3
     assert isinstance(lib.glt_last_error_string(), bytes)
 
 

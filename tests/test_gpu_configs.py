@@ -1,14 +1,16 @@
-"""The stacked-graft and bake-sentinel workloads at the Llama-3-8B MLP shape
-(hidden 4096, base intermediate 14336), with fewer tokens than the
-benchmark: the properties checked hold per token.
+"""The workloads at the Llama-3-8B shape (hidden 4096, base intermediate
+14336) at their full sizes, checked through per-token oracle samples and
+size-independent properties:
 
 * Four stacked 512-neuron slices (seeds 1..4) appended after the base
-  (N = 16384), forward only: explicit stacked grafts against the same
-  forward over shadow-baked merged weights, and against the oracle on a
-  token sample.
+  (N = 16384), 4 x 4096 tokens, forward only: explicit stacked grafts
+  against the same forward over shadow-baked merged weights on every token,
+  and against the oracle on one token of every 256-token tile.
 * shadow_bake materialising [15360,4096] / [4096,15360] baked matrices for
   several layers, then the sentinel forward (X ~N(0,1) [2048,4096]) baked
   against stacked, per layer.
+* The measured MLP step (16384 tokens) and the decoder layer with recompute
+  (2 x 4096 tokens, 32/8 heads).
 """
 import numpy as np
 import pytest
@@ -56,7 +58,7 @@ def _baked_forward(torch, ops, wg, wu, wd, slices, x, N):
 def test_stacked_four_slices_vs_baked_and_oracle(dev):
     import torch
     from glt_amd import ops
-    M, S = 1024, 512
+    M, S = 16384, 512
     N = I + 4 * S
     placements = [(I + S * k, S, 0, D) for k in range(4)]
     wg, wu, wd = _base(torch, ops)
@@ -70,14 +72,14 @@ def test_stacked_four_slices_vs_baked_and_oracle(dev):
     # accumulation order differs
     for name, a, b, q in (("gate_pre", g, gb, 2), ("up_pre", u, ub, 2), ("inter", inter, ib, 3), ("y", y, yb, 4)):
         assert_bf16_budget(to_np(a), to_np(b), q=q, what=f"stacked vs baked {name}")
-    # oracle on a token sample
-    T = 32
+    # oracle on one token of each of the 64 M-tiles (a different row of the tile each time)
+    rows = torch.tensor([256 * t + (37 * t) % 256 for t in range(M // 256)], device="cuda")
     h = lambda t: to_np(t)
     sl_np = [{"i0": s.i_start, "s": s.s, "h0": s.h_start, "h": s.h, "gate": h(s.gate), "up": h(s.up),
               "down": h(s.down)} for s in slices]
-    rg, ru, ri, ry = O.mlp_fwd(h(x[:T]), h(wg), h(wu), h(wd), N, sl_np, bf16=True)
+    rg, ru, ri, ry = O.mlp_fwd(h(x[rows]), h(wg), h(wu), h(wd), N, sl_np, bf16=True)
     for name, a, r, q in (("gate_pre", g, rg, 2), ("up_pre", u, ru, 2), ("inter", inter, ri, 3), ("y", y, ry, 4)):
-        assert_bf16_budget(to_np(a[:T]), r, q=q, what=f"stacked vs oracle {name}")
+        assert_bf16_budget(to_np(a[rows]), r, q=q, what=f"stacked vs oracle {name}")
 
 
 def test_bake_sentinel_forward(dev):
@@ -183,3 +185,109 @@ def test_config2_full_size_step_properties(dev):
         summed = parts[0][0][p].double() + parts[1][0][p].double()
         scale = full.abs().max().item()
         assert (summed - full).abs().max().item() <= 1e-5 * scale, p
+
+
+def test_config5_decoder_layer_full_size(dev):
+    """The decoder layer at its workload (2 x 4096 tokens, hidden 4096, 32
+    query / 8 kv heads of 128, RoPE theta 500000, causal; base intermediate
+    14336 plus an appended 1024-neuron slice), forward then the graft-only
+    backward with recompute on an f32 upstream gradient:
+    * forward: the layer output and the MLP input on 8 tokens (both
+      sequences, several query blocks, the last token) against the oracle's
+      composition of the reference's forward_layer (k/v of every token from
+      f64 products, attention over each sampled query's causal prefix);
+    * backward: per-token dX on those tokens against the oracle's
+      recompute (the reference's rounding) and backward; sampled dW entries
+      against f64 sums over all 8192 tokens; the two sequences' backwards
+      give the same per-token dX bit for bit and gradients that sum to the
+      whole batch's."""
+    import torch
+    from glt_amd import ops
+    bf = torch.bfloat16
+    B, T, Hq, Hkv, hd, S = 2, 4096, 32, 8, 128, 1024
+    M, N, theta, eps = B * T, I + S, 500000.0, 1e-5
+    fill = lambda shape, seed, tid, mean, std, dt=bf: ops.fill_normal(torch.empty(shape, dtype=dt, device="cuda"),
+                                                                       seed, tid, mean, std)
+    x = fill((M, D), 100, 10, 0.0, 1.0)
+    wq, wk, wv = fill((Hq * hd, D), 0, 30, 0.0, 0.02), fill((Hkv * hd, D), 0, 31, 0.0, 0.02), \
+        fill((Hkv * hd, D), 0, 32, 0.0, 0.02)
+    wo = fill((D, Hq * hd), 0, 33, 0.0, 0.02)
+    ln_in, ln_post = fill((D,), 300, 12, 1.0, 0.02), fill((D,), 300, 13, 1.0, 0.02)
+    wg, wu, wd = _base(torch, ops)
+    slices = _slices(torch, ops, [(I, S, 0, D)], seeds=(1,))
+    base = ops.BaseMLP(wg, wu, wd)
+    layer = ops.DecoderLayer(B, T, Hq, Hkv, wq, wk, wv, wo, ln_in, ln_post, base, slices, N, rope_theta=theta,
+                             rms_eps=eps)
+    x_in = x.clone()
+    out, x_ffn, _ = layer.forward(x)
+    dy = fill((M, D), 200, 11, 0.0, 1.0, torch.float32)
+    dx, grads = ops.mlp_backward(base, slices, x_ffn, dy, N, recompute=True)
+    torch.cuda.synchronize()
+    print("config-5 layer forward + backward done", flush=True)
+
+    h = lambda t: to_np(t)
+    rb = O.bf16_round
+    bi = np.array([0, 0, 0, 0, 1, 1, 1, 1])
+    ti = np.array([0, 127, 128, 2049, 1, 1000, 3968, 4095])
+    idx = bi * T + ti
+    rows = torch.tensor(idx, device="cuda")
+    xn, _ = O.rmsnorm_fwd(h(x_in), h(ln_in), eps)
+    f64 = lambda a: np.asarray(a, np.float64)
+    kv = [O.rope(rb((f64(xn) @ f64(h(w)).T).astype(np.float32)).reshape(B, T, Hkv, hd), theta, 0,
+                 exact_rounding=False) if j == 0 else rb((f64(xn) @ f64(h(w)).T).astype(np.float32)).reshape(B, T, Hkv, hd)
+          for j, w in enumerate((wk, wv))]
+    q = rb((f64(xn[idx]) @ f64(h(wq)).T).astype(np.float32)).reshape(-1, Hq, hd)
+    q = np.stack([O.rope(q[i][None, None], theta, int(ti[i]), exact_rounding=False)[0, 0] for i in range(len(idx))])
+    a = rb(O.attention_rows(q, kv[0], kv[1], bi, ti).astype(np.float32)).reshape(len(idx), Hq * hd)
+    x1 = rb(h(x_in[rows]) + rb((f64(a) @ f64(h(wo)).T).astype(np.float32)))
+    ref_ffn, _ = O.rmsnorm_fwd(x1, h(ln_post), eps)
+    sl = slices[0]
+    sl_np = [{"i0": sl.i_start, "s": sl.s, "h0": sl.h_start, "h": sl.h, "gate": h(sl.gate), "up": h(sl.up),
+              "down": h(sl.down)}]
+    wg_np, wu_np, wd_np = h(wg), h(wu), h(wd)
+    _, _, _, y = O.mlp_fwd(ref_ffn, wg_np, wu_np, wd_np, N, sl_np, bf16=True)
+    assert_bf16_budget(h(x_ffn[rows]), ref_ffn, q=4, what="config-5 MLP input")
+    assert_bf16_budget(h(out[rows]), rb(x1 + y), q=4, what="config-5 layer output")
+    del xn, kv
+
+    # backward on the sampled tokens, from the layer's own MLP input
+    xs = h(x_ffn[rows])
+    rg, ru, ri = O.mlp_recompute(xs, wg_np, wu_np, N, sl_np)
+    rdx, _ = O.mlp_bwd(xs, wg_np, wu_np, wd_np, N, sl_np, rg, ru, ri, h(dy[rows]), bf16=True)
+    assert_bf16_budget(h(dx[rows]), rdx, q=4, what="config-5 dX")
+    del wg_np, wu_np, wd_np
+
+    # sampled gradient entries over all tokens: the slice's activations (the
+    # forward's equal the recompute's for an appended slice) in f64
+    _, g, u, inter = ops.mlp_forward(base, slices, x_ffn, N)
+    torch.cuda.synchronize()
+    dyb = rb(h(dy)).astype(np.float64)                                # the graft GEMMs read bf16(dy)
+    xf = h(x_ffn).astype(np.float64)
+    dd = rb(h(sl.down)).astype(np.float64)
+    for s_ in (0, 700, 1023):
+        col = I + s_
+        it, gt, ut = (h(t[:, col]).astype(np.float64) for t in (inter, g, u))
+        di = (dyb @ dd[s_]).astype(np.float32)
+        sg = 1.0 / (1.0 + np.exp(-gt))
+        dgc = rb((di * ut * (sg * (1.0 + gt * (1.0 - sg)))).astype(np.float32)).astype(np.float64)
+        for hh in (0, 1234, 4095):
+            terms = it * dyb[:, hh]
+            got = float(grads[0][2][s_, hh])
+            assert abs(got - terms.sum()) <= 1e-4 * np.abs(terms).sum() + 1e-6, ("dW_down", s_, hh, got)
+            terms = dgc * xf[:, hh]
+            got = float(grads[0][0][s_, hh])
+            assert abs(got - terms.sum()) <= 1e-2 * np.abs(terms).sum() + 1e-6, ("dW_gate", s_, hh, got)
+    del dyb, xf, g, u, inter
+
+    # the two sequences separately
+    parts = []
+    for b in range(B):
+        xb = x_ffn[b * T:(b + 1) * T].contiguous()
+        dxb, grb = ops.mlp_backward(base, slices, xb, dy[b * T:(b + 1) * T].contiguous(), N, recompute=True)
+        torch.cuda.synchronize()
+        assert torch.equal(dxb.view(torch.int32), dx[b * T:(b + 1) * T].view(torch.int32))
+        parts.append(grb)
+    for p in range(3):
+        full = grads[0][p].double()
+        summed = parts[0][0][p].double() + parts[1][0][p].double()
+        assert (summed - full).abs().max().item() <= 1e-5 * full.abs().max().item(), p

@@ -156,6 +156,55 @@ def test_bake_materialize_bitexact(dev, gdt):
             np.testing.assert_array_equal(_bits(dev_b[l][p]), O.f32_to_bf16_bits(bases[l][p]))
 
 
+@pytest.mark.parametrize("materialize", [True, False])
+def test_bake_seven_slices_eighteen_layers(dev, materialize):
+    """As many slices as the MLP path stacks (7) and more layers than one
+    launch takes (18 > 16): materialised (4 appended + 3 in-place slices) and
+    in place (7 in-place slices), bit-exact against numpy."""
+    import torch
+    from glt_amd import _ffi, ops
+    L, D, I = 18, 256, 384
+    if materialize:
+        pl = [(384, 32, 0, 256), (416, 32, 64, 128), (448, 32, 0, 64), (480, 32, 32, 200),
+              (0, 16, 0, 64), (40, 24, 72, 40), (100, 8, 200, 56)]
+        N = 512
+    else:
+        pl = [(0, 16, 0, 64), (40, 24, 72, 40), (100, 8, 200, 56), (128, 64, 0, 256), (200, 40, 8, 24),
+              (300, 50, 100, 156), (360, 24, 250, 6)]
+        N = I
+    rng = np.random.default_rng(11)
+    bases = [[O.bf16_round(rng.normal(0, 0.02, sh).astype(np.float32)) for sh in ((I, D), (I, D), (D, I))]
+             for _ in range(L)]
+    grafts = [[rng.normal(0, 0.02, (3, sz, h)).astype(np.float32) for _ in range(L)] for (i0, sz, h0, h) in pl]
+    dev_b = [[to_dev(b, torch.bfloat16) for b in lay] for lay in bases]
+    st = _ffi.ModelState(0)
+    if materialize:
+        outs = [[torch.empty((N, D), dtype=torch.bfloat16, device=dev) for _ in range(L)] for _ in range(2)] + \
+               [[torch.empty((D, N), dtype=torch.bfloat16, device=dev) for _ in range(L)]]
+    else:
+        outs = [[b[p] for b in dev_b] for p in range(3)]
+    ops.shadow_bake(st, [b[0] for b in dev_b], [b[1] for b in dev_b], [b[2] for b in dev_b],
+                    [[to_dev(g.ravel(), torch.float32) for g in per] for per in grafts], pl, D=D, I=I, N=N,
+                    materialize=materialize, gate_out=outs[0] if materialize else None,
+                    up_out=outs[1] if materialize else None, down_out=outs[2] if materialize else None)
+    torch.cuda.synchronize()
+    assert st.baked == 1
+    for l in range(L):
+        for p in range(3):
+            ref = np.zeros((N, D) if p < 2 else (D, N), np.float32)
+            if p < 2:
+                ref[:I] = bases[l][p]
+            else:
+                ref[:, :I] = bases[l][p]
+            for j, (i0, sz, h0, h) in enumerate(pl):
+                blk = grafts[j][l][p]
+                if p < 2:
+                    ref[i0:i0 + sz, h0:h0 + h] += blk
+                else:
+                    ref[h0:h0 + h, i0:i0 + sz] += blk.T
+            np.testing.assert_array_equal(_bits(outs[p][l]), O.f32_to_bf16_bits(ref), err_msg=f"{l} {p}")
+
+
 # ---------------------------------------------------------------- RMSNorm
 @pytest.mark.parametrize("M,D", [(64, 4096), (33, 513), (16, 8192)])
 def test_rmsnorm(dev, M, D):
@@ -249,6 +298,43 @@ def test_adamw_graft_step_refreshes_packed_mirror(dev, S, H):
         np.testing.assert_array_equal(rowmajor[2 * p + 1], wb.T)
         np.testing.assert_array_equal(shuf[2 * p], shuffle_b(wb))
         np.testing.assert_array_equal(shuf[2 * p + 1], shuffle_b(wb.T))
+
+
+@pytest.mark.parametrize("clip", [1.0, 1e6])
+def test_adamw_graft_step_global_clip(dev, clip):
+    """The graft step's clip is one global L2 norm over every updated
+    projection of every slice (the reference's clip over all of its deltas,
+    grafting.hip:1149-1164): two slices (the fused mirror kernel and the
+    separate-pass shape) against the oracle's clipped AdamW over the
+    concatenated gradients; clip 1e6 leaves the update unclipped."""
+    import torch
+    from glt_amd import ops
+    shapes = [(64, 128), (64, 96)]
+    slices, grads, ms, vs, w0, gs = [], [], [], [], [], []
+    for j, (S, H) in enumerate(shapes):
+        masters = [torch.from_numpy(draw((S, H), 20 + j, p, 0, 0.02, bf16=False)).cuda() for p in range(3)]
+        w0.append([to_np(t).copy() for t in masters])
+        slices.append(ops.GraftSlice(0, S, 0, H, *masters).pack())
+        g = draw((3 * S * H,), 30 + j, 1, 0, 0.05, bf16=False)   # global norm ~ 14, clipped at 1.0
+        gs.append(g)
+        grads.append(torch.from_numpy(g).cuda())
+        ms.append(torch.zeros(3 * S * H, device=dev))
+        vs.append(torch.zeros(3 * S * H, device=dev))
+    ops.adamw_graft_step(slices, grads, ms, vs, 2, 1e-3, clip_norm=clip)
+    torch.cuda.synchronize()
+    allg = np.concatenate(gs)
+    allw = np.concatenate([np.concatenate([a.ravel() for a in w]) for w in w0])
+    z = np.zeros_like(allw)
+    rw, rm, rv = O.adamw(allw, allg, z, z, 2, 1e-3, 0.9, 0.999, 1e-8, 0.01, clip_norm=clip)
+    got_w = np.concatenate([np.concatenate([to_np(t).ravel() for t in (sl.gate, sl.up, sl.down)]) for sl in slices])
+    assert_f32_close(got_w, rw, tol=1e-6, what="w")
+    assert_f32_close(np.concatenate([to_np(t) for t in ms]), rm, tol=1e-5, what="m")
+    assert_f32_close(np.concatenate([to_np(t) for t in vs]), rv, tol=1e-5, what="v")
+    unclipped = O.adamw(allw, allg, z, z, 2, 1e-3, 0.9, 0.999, 1e-8, 0.01)[1]
+    assert (np.abs(rm - unclipped).max() > 1e-3 * np.abs(unclipped).max()) == (clip == 1.0)
+    for sl in slices:   # the mirrors follow the clipped masters
+        rowmajor, _ = packed_views(O.bf16_bits_to_f32(_bits(sl.packed)), sl.s, sl.h)
+        np.testing.assert_array_equal(rowmajor[0], O.bf16_round(to_np(sl.gate)))
 
 
 def test_base_prepare_layout(dev):

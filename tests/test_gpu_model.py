@@ -71,19 +71,88 @@ def test_model_forward_matches_oracle(dev, explicit):
     assert_bf16_budget(to_np(logits), ref, q=8, what="logits")
 
 
-def test_eval_stats_match_oracle(dev):
+@pytest.mark.parametrize("reference_hash", [True, False])
+def test_eval_stats_match_oracle(dev, reference_hash):
     import torch
     from glt_amd import ops
     B, T, V = 2, 33, 1500
     x = O.bf16_round(np.random.default_rng(8).normal(0, 3, (B * T, V)).astype(np.float32))
     ids = np.random.default_rng(9).integers(0, V, (B, T)).astype(np.int32)
-    r = ops.eval_stats(to_dev(x, torch.bfloat16), torch.tensor(ids).cuda())
-    ref = O.eval_stats(x.reshape(B, T, V), ids)
+    r = ops.eval_stats(to_dev(x, torch.bfloat16), torch.tensor(ids).cuda(), reference_hash=reference_hash)
+    ref = O.eval_stats(x.reshape(B, T, V), ids, reference_hash=reference_hash)
     assert r["logits_hash"] == ref["logits_hash"]
     assert r["count"] == ref["count"]
     assert r["total_nll"] == pytest.approx(ref["total_nll"], rel=1e-5)
     assert r["logits_sum"] == pytest.approx(ref["logits_sum"], rel=1e-9, abs=1e-6)
     assert r["logits_sumsq"] == pytest.approx(ref["logits_sumsq"], rel=1e-12)
+
+
+@pytest.mark.parametrize("B,T,V,ld", [(2, 3, 128256, 128256),   # the Llama-3 vocabulary, 16-byte chunks
+                                      (3, 5, 1001, 1001),       # odd rows: element-wise walk
+                                      (1, 2, 7, 7),             # fewer logits than chunks per row
+                                      (2, 4, 96, 104),          # padded row stride
+                                      (4, 512, 32000, 32000)])  # 32768 chunks: several scan workgroups
+def test_eval_reference_hash_is_exact(dev, B, T, V, ld):
+    """The reference's logits hash (one FNV-1a chain over every f32 logit byte,
+    grafting.hip:536-546) bit for bit, from the basis and from an arbitrary
+    running hash, against the oracle's sequential loop."""
+    import torch
+    from glt_amd import ops
+    rng = np.random.default_rng(B * 1000 + V)
+    x = O.bf16_round(rng.normal(0, 2, (B * T, ld)).astype(np.float32))
+    ids = rng.integers(0, V, (B, T)).astype(np.int32)
+    xd, idd = to_dev(x, torch.bfloat16), torch.tensor(ids).cuda()
+    view = xd[:, :V]
+    h0 = int(rng.integers(0, 2 ** 63)) * 2 + 1
+    for hin in (O.FNV_BASIS, h0):
+        r = ops.eval_stats(view, idd, hash_in=hin)
+        assert r["logits_hash"] == O.eval_hash_reference(x[:, :V].reshape(B, T, V), hin), (B, T, V, hin)
+    print("hash", B, T, V, hex(r["logits_hash"]), flush=True)
+
+
+def test_eval_reference_hash_chains_batches(dev):
+    """Batches chained as the reference's eval loop does (the running hash
+    carries over): eval_batches over three batches equals the sequential
+    chain over their concatenation, and nll/counts add up."""
+    import torch
+    from glt_amd import ops
+    rng = np.random.default_rng(12)
+    V, T = 5000, 17
+    xs = [O.bf16_round(rng.normal(0, 3, (b, T, V)).astype(np.float32)) for b in (2, 1, 3)]
+    ids = [rng.integers(0, V, (x.shape[0], T)).astype(np.int32) for x in xs]
+    r = ops.eval_batches([(to_dev(x.reshape(-1, V), torch.bfloat16), torch.tensor(i).cuda()) for x, i in zip(xs, ids)])
+    assert r["logits_hash"] == O.eval_hash_reference(np.concatenate(xs))
+    refs = [O.eval_stats(x, i) for x, i in zip(xs, ids)]
+    assert r["count"] == sum(q["count"] for q in refs)
+    assert r["total_nll"] == pytest.approx(sum(q["total_nll"] for q in refs), rel=1e-5)
+
+
+def test_lm_head_at_eval_size_runs_in_row_blocks(dev):
+    """An LM head whose logits pass 2 GiB (16384 tokens x 128256 = 4 GiB of
+    bf16) runs on the MFMA kernel in row blocks of 7936 tokens (the most
+    whose output offsets fit the kernel's 31-bit buffer range: three launches
+    here) instead of falling back to the strided kernel; sampled rows of every
+    block match the oracle."""
+    import torch
+    from glt_amd import _ffi as F
+    from glt_amd import ops
+    M, D, V = 16384, 4096, 128256
+    bf = torch.bfloat16
+    x = ops.fill_normal(torch.empty((M, D), dtype=bf, device="cuda"), 100, 10, 0.0, 1.0)
+    w = ops.fill_normal(torch.empty((V, D), dtype=bf, device="cuda"), 0, 60, 0.0, 0.02)
+    prep = torch.empty(F.load().glt_lm_head_prepared_size(V, D), dtype=torch.uint8, device="cuda")
+    F.call("glt_lm_head_prepare", ops._p(w), V, D, ops._p(prep), ops._stream())
+    F.load().glt_profile_enable(1)
+    F.profile_collect()
+    logits = ops.lm_head_fwd(x, w, prep)
+    torch.cuda.synchronize()
+    prof = F.profile_collect()
+    F.load().glt_profile_enable(0)
+    assert prof["lm_head"][1] == 3, prof
+    rows = torch.tensor([0, 4095, 7935, 7936, 12000, 15871, 15872, 16383], device="cuda")
+    wn = to_np(w)
+    ref = O.lm_head(to_np(x[rows]), wn)
+    assert_bf16_budget(to_np(logits[rows]), ref, q=1, what="eval-size logits")
 
 
 def test_certify_bake_and_reload_gates(dev):

@@ -37,16 +37,18 @@ def test_eval_hash_is_order_and_value_sensitive():
     rng = np.random.default_rng(2)
     x = O.bf16_round(rng.normal(0, 1, (1, 4, 16)).astype(np.float32))
     ids = np.zeros((1, 4), np.int32)
-    h = O.eval_stats(x, ids)["logits_hash"]
-    y = x.copy()
-    y[0, 2, 5] = np.nextafter(y[0, 2, 5], np.float32(np.inf))
-    assert O.eval_stats(y, ids)["logits_hash"] != h
-    z = x[:, ::-1].copy()
-    assert O.eval_stats(z, ids)["logits_hash"] != h
-    # one row of 16: sixteen one-element chunks, each hashed from the basis,
-    # the chunk hashes' bytes hashed in order, then that row hash's 8 bytes
+    for ref in (True, False):
+        h = O.eval_stats(x, ids, reference_hash=ref)["logits_hash"]
+        y = x.copy()
+        y[0, 2, 5] = np.nextafter(y[0, 2, 5], np.float32(np.inf))
+        assert O.eval_stats(y, ids, reference_hash=ref)["logits_hash"] != h
+        z = x[:, ::-1].copy()
+        assert O.eval_stats(z, ids, reference_hash=ref)["logits_hash"] != h
+    # row form. One row of 16: sixteen one-element chunks, each hashed from
+    # the basis, the chunk hashes' bytes hashed in order, then that row
+    # hash's 8 bytes
     fb = lambda a: a.astype("<f4").tobytes()
-    r = O.eval_stats(x[:, :1], ids[:, :1])["logits_hash"]
+    r = O.eval_stats(x[:, :1], ids[:, :1], reference_hash=False)["logits_hash"]
     chunks = b"".join(O.fnv1a64(fb(x[0, 0, c:c + 1])).to_bytes(8, "little") for c in range(16))
     assert r == O.fnv1a64(O.fnv1a64(chunks).to_bytes(8, "little"))
     # 20 elements: ten chunks of two, six empty chunks (an empty chunk hashes to the basis)
@@ -67,3 +69,75 @@ def test_certify_gates():
     assert ops.certify(A, {"ce": 2.0, "logits_hash": 8}, {"ce": 2.0, "logits_hash": 9}, dict(A))["content"] == \
         "B_BAKED_MISLABEL_SUSPECT"
     assert ops.certify(A, B, C, {"ce": 2.0, "logits_hash": 6})["gate_reload_equal"] == 0
+
+
+def _reference_hash_loop(logits, h=O.FNV_BASIS):
+    """The reference's loop written out (grafting.hip:536-546): for b, t, v
+    the f32 logit's four bytes in memory order, h ^= byte; h *= prime."""
+    B, T, V = logits.shape
+    for b in range(B):
+        for t in range(T):
+            for v in range(V):
+                for byte in np.float32(logits[b, t, v]).tobytes():   # little-endian on x86-64
+                    h = ((h ^ byte) * 1099511628211) % (1 << 64)
+    return h
+
+
+def test_eval_reference_hash_is_the_sequential_byte_chain():
+    """The oracle's reference hash (through the C FNV) equals the reference's
+    loop written out, continues from any start (the reference chains its
+    eval batches), and its C FNV agrees with the published vectors."""
+    rng = np.random.default_rng(3)
+    x = O.bf16_round(rng.normal(0, 3, (2, 3, 37)).astype(np.float32))
+    assert O.eval_hash_reference(x) == _reference_hash_loop(x)
+    h1 = O.eval_hash_reference(x[:1])
+    assert O.eval_hash_reference(x[1:], h1) == O.eval_hash_reference(x)
+    assert O.eval_stats(x, np.zeros((2, 3), np.int32))["logits_hash"] == _reference_hash_loop(x)
+    assert O.fnv1a64_c(b"foobar", O.FNV_BASIS_PUBLISHED) == 0x85944171f73967e8
+    data = rng.integers(0, 256, 1000).astype(np.uint8).tobytes()
+    assert O.fnv1a64_c(data, 12345) == O.fnv1a64(data, 12345)
+
+
+def _parallel_hash(bits16, h, chunks):
+    """The decomposition the GPU computes, restated on the CPU: the low byte
+    of the state is a chain of its own (low nibble first, then high nibble,
+    each a 16-state map per chunk composed in order), after which each chunk
+    is the affine map h -> h * P^(4n) + B mod 2^64."""
+    P, M64 = 1099511628211, (1 << 64) - 1
+
+    def run8(c, s):
+        for w in c:
+            s = (s * P * P) & 0xFF
+            s = ((s ^ (int(w) & 0xFF)) * P) & 0xFF
+            s = ((s ^ (int(w) >> 8)) * P) & 0xFF
+        return s
+
+    def run64(c, hh):
+        for w in c:
+            for byte in (0, 0, int(w) & 0xFF, int(w) >> 8):
+                hh = ((hh ^ byte) * P) & M64
+        return hh
+
+    n = -(-len(bits16) // chunks)
+    cs = [bits16[i * n:(i + 1) * n] for i in range(chunks)]
+    lo, s_lo = h & 15, []
+    for c in cs:
+        s_lo.append(lo)
+        lo = [run8(c, i) & 15 for i in range(16)][lo]
+    hi, s8 = (h >> 4) & 15, []
+    for c, l in zip(cs, s_lo):
+        s8.append((hi << 4) | l)
+        hi = [run8(c, (i << 4) | l) >> 4 for i in range(16)][hi]
+    for c, s in zip(cs, s8):
+        a = pow(P, 4 * len(c), 1 << 64)
+        h = (h * a + (run64(c, s) - s * a)) & M64
+    return h
+
+
+def test_parallel_hash_decomposition_reproduces_the_chain():
+    rng = np.random.default_rng(4)
+    for n, chunks in ((1, 1), (50, 7), (333, 16), (64, 64)):
+        x = O.bf16_round(rng.normal(0, 2, n).astype(np.float32))
+        bits = O.f32_to_bf16_bits(x)
+        for h in (O.FNV_BASIS, int(rng.integers(0, 2 ** 63)) * 2 + 1):
+            assert _parallel_hash(bits, h, chunks) == O.eval_hash_reference(x, h)

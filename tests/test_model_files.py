@@ -144,3 +144,17 @@ def test_f16_subnormals_and_specials_convert_exactly(tmp_path):
         assert torch.equal(got, t.float())
         assert torch.equal(m.read("h", torch.bfloat16, device="cpu").view(torch.int16),
                            t.float().to(torch.bfloat16).view(torch.int16))
+
+
+def test_wrapping_element_count_is_refused(tmp_path):
+    """A header whose element count times the element size wraps around
+    64 bits to the stored byte count (F32 [1, 2^62 + 1] over 4 bytes) is
+    malformed; opening it fails with GLT_ERR_FORMAT instead of letting a
+    later read size its copy from the wrapped product."""
+    header = json.dumps({"w": {"dtype": "F32", "shape": [1, 2 ** 62 + 1], "data_offsets": [0, 4]}}).encode()
+    header += b" " * (-len(header) % 8)
+    path = tmp_path / "wrap.safetensors"
+    path.write_bytes(struct.pack("<Q", len(header)) + header + b"\0" * 4)
+    with pytest.raises(F.GltError) as e:
+        ops.SafetensorsModel(path)
+    assert e.value.status == "GLT_ERR_FORMAT"

@@ -359,3 +359,49 @@ def test_test6_f32_explicit_equals_baked_oracle():
     for u, v in zip(a, b):
         md = np.max(np.abs(u - v))
         assert md < G["tol_abs"] or md / np.max(np.abs(v)) < G["tol_rel"]
+
+
+def test_attention_rows_equals_full_attention():
+    """The sampled-query form gives the full form's rows (causal and not)."""
+    B, T, Hq, Hkv, hd = 2, 23, 4, 2, 8
+    rng = np.random.default_rng(9)
+    q, k, v = (rng.normal(size=(B, T, H, hd)) for H in (Hq, Hkv, Hkv))
+    bi, ti = np.array([0, 0, 1, 1, 1]), np.array([0, 11, 3, 21, 22])
+    for causal in (True, False):
+        full = O.attention(q, k, v, causal=causal)
+        rows = O.attention_rows(q[bi, ti], k, v, bi, ti, causal=causal)
+        np.testing.assert_allclose(rows, full[bi, ti], rtol=1e-12, atol=1e-14)
+
+
+def test_mlp_recompute_matches_aten_bf16_sequence():
+    """The reference's recompute (src/layer_recompute_impl.inc:20-64) rebuilds
+    each grafted slice of the bf16 pre-activation with torch's bf16 in-place
+    add of the cached delta cast to bf16. The oracle's recompute equals that
+    sequence run with torch's CPU bf16 kernels on the oracle's own base
+    pre-activations and delta GEMMs; the forward (one rounding of the f32
+    delta) differs from it on in-place slices and equals it on appended ones."""
+    D, I, N, M = 32, 48, 64, 40
+    rng = np.random.default_rng(21)
+    x = O.bf16_round(rng.normal(size=(M, D)).astype(np.float32))
+    wg, wu = (O.bf16_round(rng.normal(0, 0.2, (I, D)).astype(np.float32)) for _ in range(2))
+    wd = O.bf16_round(rng.normal(0, 0.2, (D, I)).astype(np.float32))
+    sl = [{"i0": 8, "s": 16, "h0": 4, "h": 20},      # in place
+          {"i0": 48, "s": 16, "h0": 0, "h": 32}]     # appended
+    for s in sl:
+        for p in ("gate", "up", "down"):
+            s[p] = rng.normal(0, 0.3, (s["s"], s["h"])).astype(np.float32)
+    g, u, inter = O.mlp_recompute(x, wg, wu, N, sl)
+    gb, ub, _, _ = O.mlp_fwd(x, wg, wu, wd, N, [], bf16=True)        # base pre-activations (bf16)
+    for name, got, base in (("gate", g, gb), ("up", u, ub)):
+        t = torch.from_numpy(base.copy()).to(torch.bfloat16)
+        for s in sl:
+            # the cached expand output: f32 delta of the forward (graft GEMM kind 0)
+            delta = O.graft_gemm(0, M, s["s"], s["h"], a=x[:, s["h0"]:s["h0"] + s["h"]].copy(), lda=s["h"],
+                                 delta=s[name])
+            t[:, s["i0"]:s["i0"] + s["s"]].add_(torch.from_numpy(delta).to(torch.bfloat16))
+        np.testing.assert_array_equal(got, t.float().numpy(), err_msg=name)
+    np.testing.assert_array_equal(inter, O.silu_mul(g, u))
+    gf, uf, _, _ = O.mlp_fwd(x, wg, wu, wd, N, sl, bf16=True)
+    np.testing.assert_array_equal(g[:, I:], gf[:, I:])                 # appended: one rounding either way
+    assert np.any(g[:, 8:24] != gf[:, 8:24])                           # in place: the double rounding shows
+    assert np.max(np.abs(g - gf)) <= 2 ** -7 * np.max(np.abs(gf))      # within one bf16 ulp of the forward
