@@ -48,8 +48,11 @@ STEP_FLOP = sum(GEMM_FLOP.values())
 HBM_BYTES = {
     "rmsnorm_fwd": 2 * M * D * 2 + D * 2 + M * 4,          # x in, y out (bf16), gamma, mean-square out
     "rmsnorm_bwd": M * D * (4 + 2 + 4) + D * 2 + M * 4,    # dy f32, x bf16 in, dx f32 out, gamma, mean-square
-    # one projection: w, g, m, v in; w, m, v out; the four bf16 mirrors out
-    "adamw_pack": S * D * (4 * 4 + 3 * 4 + 4 * 2),
+    # the slice's three projections in one launch: w, g, m, v in; w, m, v
+    # out; the four bf16 mirrors out
+    "adamw_pack": 3 * S * D * (4 * 4 + 3 * 4 + 4 * 2),
+    # the clip's sum of squares over the three projections' gradients
+    "clip_sumsq": 3 * S * D * 4,
 }
 ROPE_B, ROPE_T, ROPE_HQ, ROPE_HK, ROPE_HD, ROPE_THETA = 2, 4096, 32, 8, 128, 500000.0
 # masked cross-entropy bench: 4 x 4096 tokens, Llama-3 vocabulary
@@ -204,8 +207,7 @@ def main():
     # step, RoPE at the decoder-layer shape (2 x 4096 tokens, 32 q / 8 kv
     # heads of 128, theta 5e5)
     hbm = {}
-    for k, nbytes in (("rmsnorm_fwd", HBM_BYTES["rmsnorm_fwd"]), ("rmsnorm_bwd", HBM_BYTES["rmsnorm_bwd"]),
-                      ("adamw_pack", HBM_BYTES["adamw_pack"])):
+    for k, nbytes in HBM_BYTES.items():
         if k in kernels:
             t = kernels[k]["avg_ms"]
             hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),

@@ -25,9 +25,21 @@ __global__ void __launch_bounds__(256) sumsq_partial_kernel(const ClipSegs segs,
   __shared__ float wsum[4];
   float s = 0.f;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (int j = 0; j < segs.nseg; ++j) {
     const float* g = segs.g[j];
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < segs.n[j]; i += stride) s += g[i] * g[i];
+    const int64_t n = segs.n[j];
+    int64_t done = 0;
+    if ((reinterpret_cast<uintptr_t>(g) & 15) == 0) {
+      // 16-byte loads over the whole multiple-of-4 prefix
+      const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
+      for (int64_t i = first; i < n / 4; i += stride) {
+        const f32x4 v = g4[i];
+        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+      done = n / 4 * 4;
+    }
+    for (int64_t i = done + first; i < n; i += stride) s += g[i] * g[i];
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
@@ -37,10 +49,10 @@ __global__ void __launch_bounds__(256) sumsq_partial_kernel(const ClipSegs segs,
 }
 
 // scale = clip/norm if norm > clip else 1, norm = sqrt(sum + 1e-8)
-// (reference calc_scale_kernel, src/kernels_elementwise_impl.inc:170-197):
-// one workgroup adds the partials in a fixed order and writes the scale.
-__global__ void __launch_bounds__(256) clip_scale_kernel(const float* __restrict__ partial, int np, float clip,
-                                                         float* __restrict__ scale) {
+// (reference calc_scale_kernel, src/kernels_elementwise_impl.inc:170-197).
+// Every workgroup of an update kernel adds the np partials in the same
+// fixed order, so all of them get the same scale without a launch of its own.
+__device__ float block_clip_scale(const float* __restrict__ partial, int np, float clip) {
   __shared__ float wsum[4];
   float s = 0.f;
   for (int i = threadIdx.x; i < np; i += 256) s += partial[i];
@@ -48,23 +60,28 @@ __global__ void __launch_bounds__(256) clip_scale_kernel(const float* __restrict
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const float norm = sqrtf(wsum[0] + wsum[1] + wsum[2] + wsum[3] + 1e-8f);
-    scale[0] = norm > clip ? clip / norm : 1.0f;
-  }
+  const float norm = sqrtf(wsum[0] + wsum[1] + wsum[2] + wsum[3] + 1e-8f);
+  return norm > clip ? clip / norm : 1.0f;
 }
 
-// Launches the two clip kernels over segs; scale lands in ws[kClipBlocks].
-glt_status launch_clip(const ClipSegs& segs, float clip, float* ws, hipStream_t st) {
+// The partials of a clip over segs: ws[0, np). Returns np through *np_out.
+glt_status launch_clip(const ClipSegs& segs, float* ws, size_t ws_floats, int* np_out, hipStream_t st) {
   int64_t total = 0;
   for (int j = 0; j < segs.nseg; ++j) total += segs.n[j];
-  const int np = (int)std::max<int64_t>(1, std::min<int64_t>(kClipBlocks, cdiv(total, 256)));
+  const int np = (int)std::max<int64_t>(1, std::min<int64_t>(kClipBlocks, cdiv(total, 1024)));
+  GLT_CHECK((size_t)np <= ws_floats, GLT_ERR_WORKSPACE, "adamw clip: %d partial sums, room for %zu", np, ws_floats);
   GLT_LAUNCH("clip_sumsq", sumsq_partial_kernel, dim3(np), dim3(256), 0, st, segs, ws);
   GLT_LAUNCH_CHECK("sumsq_partial");
-  GLT_LAUNCH("clip_scale", clip_scale_kernel, dim3(1), dim3(256), 0, st, ws, np, clip, ws + kClipBlocks);
-  GLT_LAUNCH_CHECK("clip_scale");
+  *np_out = np;
   return GLT_OK;
 }
+
+// Clip inputs of an update kernel: partial == nullptr means no clip.
+struct ClipIn {
+  const float* partial;
+  int np;
+  float clip;
+};
 
 // One AdamW element update in the reference's operation order
 // (reference adamw_fused_kernel, src/kernels_optimizer_impl.inc:27-51).
@@ -81,8 +98,8 @@ __global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ w, const
                                                     float* __restrict__ m, float* __restrict__ v,
                                                     uint16_t* __restrict__ mirror, int64_t n, float lr,
                                                     float b1, float b2, float b1c, float b2c, float eps,
-                                                    float wd, const float* __restrict__ clip_scale) {
-  const float scale = clip_scale ? *clip_scale : 1.0f;
+                                                    float wd, const ClipIn ci) {
+  const float scale = ci.partial ? block_clip_scale(ci.partial, ci.np, ci.clip) : 1.0f;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     float mi = m[i], vi = v[i];
@@ -94,24 +111,47 @@ __global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ w, const
   }
 }
 
-// AdamW over one [S, H] graft projection fused with the refresh of its four
+// AdamW over [S, H] graft projections fused with the refresh of their four
 // bf16 mirrors in the packed slice: row-major [S,H], row-major [H,S], and
 // the fragment layout of both. One workgroup per 64 x 64 tile (S and H
-// multiples of 64, so no fragment block is padded): the f32 state streams
-// through registers as 16-byte accesses, the new weights go through LDS
-// once, and every mirror is written with 16-byte stores. The master is read
-// once instead of once per mirror.
-__global__ void __launch_bounds__(256) adamw_pack_kernel(float* __restrict__ w, const float* __restrict__ g,
-                                                         float* __restrict__ m, float* __restrict__ v, int S,
-                                                         int H, float lr, float b1, float b2, float b1c,
-                                                         float b2c, float eps, float wd,
-                                                         const float* __restrict__ clip_scale,
-                                                         uint16_t* __restrict__ rm, uint16_t* __restrict__ rmt,
-                                                         uint16_t* __restrict__ sh, uint16_t* __restrict__ sht) {
+// multiples of 64, so no fragment block is padded), the tiles of every
+// projection of a step in one launch: the f32 state streams through
+// registers as 16-byte accesses, the new weights go through LDS once, and
+// every mirror is written with 16-byte stores. The master is read once
+// instead of once per mirror.
+constexpr int kMaxPackJobs = kClipMaxSegs;
+struct PackJob {
+  float* w;
+  const float* g;
+  float* m;
+  float* v;
+  uint16_t* rm;   // row-major [S,H]
+  uint16_t* rmt;  // row-major [H,S]
+  uint16_t* sh;   // fragment layout of [S,H]
+  uint16_t* sht;  // fragment layout of [H,S]
+  int S, H;
+  int tile0;      // first workgroup of this projection
+};
+struct PackJobs {
+  PackJob j[kMaxPackJobs];
+  int n;
+};
+
+__global__ void __launch_bounds__(256) adamw_pack_kernel(const PackJobs jobs, float lr, float b1, float b2, float b1c,
+                                                         float b2c, float eps, float wd, const ClipIn ci) {
   __shared__ float tile[64][65];
-  const float scale = clip_scale ? *clip_scale : 1.0f;
+  const float scale = ci.partial ? block_clip_scale(ci.partial, ci.np, ci.clip) : 1.0f;
+  int jb = 0;
+  while (jb + 1 < jobs.n && (int)blockIdx.x >= jobs.j[jb + 1].tile0) ++jb;
+  const PackJob& J = jobs.j[jb];
+  float* __restrict__ w = J.w;
+  const float* __restrict__ g = J.g;
+  float* __restrict__ m = J.m;
+  float* __restrict__ v = J.v;
+  const int S = J.S, H = J.H;
   const int hb = H / 64;
-  const int r0 = (blockIdx.x / hb) * 64, c0 = (blockIdx.x % hb) * 64;
+  const int bt = (int)blockIdx.x - J.tile0;
+  const int r0 = (bt / hb) * 64, c0 = (bt % hb) * 64;
   const int t = threadIdx.x;
   {
     const int rr = t >> 4, c4 = (t & 15) * 4;
@@ -136,14 +176,14 @@ __global__ void __launch_bounds__(256) adamw_pack_kernel(float* __restrict__ w, 
       u32x2 q;
       q.x = pack_bf16x2(nw[0], nw[1]);
       q.y = pack_bf16x2(nw[2], nw[3]);
-      *reinterpret_cast<u32x2*>(rm + o) = q;
+      *reinterpret_cast<u32x2*>(J.rm + o) = q;
     }
   }
   __syncthreads();
   {
     // [H,S] row-major: column c of the tile, 16 consecutive rows per thread
     const int c = t >> 2, rs = (t & 3) * 16;
-    uint16_t* dst = rmt + (int64_t)(c0 + c) * S + r0 + rs;
+    uint16_t* dst = J.rmt + (int64_t)(c0 + c) * S + r0 + rs;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       u32x4 q;
@@ -169,8 +209,8 @@ __global__ void __launch_bounds__(256) adamw_pack_kernel(float* __restrict__ w, 
       }
       const int64_t blk = (int64_t)(r0 / 32 + half) * hb + c0 / 64;
       const int64_t blkt = (int64_t)(c0 / 32 + half) * (S / 64) + r0 / 64;
-      *reinterpret_cast<u32x4*>(sh + blk * kShufBlock + t * 8) = q;
-      *reinterpret_cast<u32x4*>(sht + blkt * kShufBlock + t * 8) = qt;
+      *reinterpret_cast<u32x4*>(J.sh + blk * kShufBlock + t * 8) = q;
+      *reinterpret_cast<u32x4*>(J.sht + blkt * kShufBlock + t * 8) = qt;
     }
   }
 }
@@ -188,7 +228,7 @@ using namespace glt;
 
 extern "C" {
 
-size_t glt_adamw_workspace_size(int64_t n) { return (size_t)(kClipBlocks + 64) * sizeof(float); }
+size_t glt_adamw_workspace_size(int64_t n) { return (size_t)kClipBlocks * sizeof(float); }
 
 glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* mirror, int64_t n, int32_t step,
                           float lr, float beta1, float beta2, float eps, float weight_decay, float clip_norm,
@@ -197,7 +237,7 @@ glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* mirr
   GLT_CHECK(n == 0 || (w && g && m && v), GLT_ERR_INVALID_ARG, "glt_adamw_step: null pointer");
   if (n == 0) return GLT_OK;
   hipStream_t st = as_stream(stream);
-  const float* scale = nullptr;
+  ClipIn ci{nullptr, 0, clip_norm};
   if (clip_norm > 0.f) {
     GLT_CHECK(ws && ws_bytes >= glt_adamw_workspace_size(n), GLT_ERR_WORKSPACE,
               "glt_adamw_step: clip needs %zu workspace bytes", glt_adamw_workspace_size(n));
@@ -205,32 +245,33 @@ glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* mirr
     segs.g[0] = g;
     segs.n[0] = n;
     segs.nseg = 1;
-    glt_status s = launch_clip(segs, clip_norm, static_cast<float*>(ws), st);
+    glt_status s = launch_clip(segs, static_cast<float*>(ws), ws_bytes / sizeof(float), &ci.np, st);
     if (s != GLT_OK) return s;
-    scale = static_cast<const float*>(ws) + kClipBlocks;
+    ci.partial = static_cast<const float*>(ws);
   }
   // bias corrections as the reference computes them on the host
   // (src/kernels_optimizer_impl.inc:64-65)
   const float b1c = 1.0f / (1.0f - powf(beta1, (float)(step + 1)));
   const float b2c = 1.0f / (1.0f - powf(beta2, (float)(step + 1)));
   GLT_LAUNCH("adamw", adamw_kernel, dim3(grid_n(n)), dim3(256), 0, st, w, g, m, v, mirror, n, lr, beta1, beta2,
-                     b1c, b2c, eps, weight_decay, scale);
+                     b1c, b2c, eps, weight_decay, ci);
   GLT_LAUNCH_CHECK("adamw");
   return GLT_OK;
 }
 
 namespace glt {
-// The graft step over caller-provided clip memory (kClipBlocks + 1 floats).
+// The graft step; the clip's partial sums go to clip_ws (clip_ws_floats
+// floats, at least kClipBlocks).
 static glt_status graft_step(const glt_graft_slice* slices, int32_t n_slices, float* const* grads, float* const* m,
                              float* const* v, uint16_t* const* packed_out, int32_t proj_mask, int32_t step, float lr,
                              float beta1, float beta2, float eps, float weight_decay, float clip_norm,
-                             float* clip_ws, hipStream_t st) {
+                             float* clip_ws, size_t clip_ws_floats, hipStream_t st) {
   GLT_CHECK(n_slices >= 0 && n_slices <= kClipMaxSegs / 3, GLT_ERR_UNSUPPORTED,
             "glt_adamw_graft_step: %d slices (max %d)", n_slices, kClipMaxSegs / 3);
   GLT_CHECK(n_slices == 0 || (slices && grads && m && v), GLT_ERR_INVALID_ARG, "glt_adamw_graft_step: null pointer");
   for (int j = 0; j < n_slices; ++j)
     GLT_CHECK(grads[j] && m[j] && v[j], GLT_ERR_INVALID_ARG, "glt_adamw_graft_step: null state of slice %d", j);
-  const float* scale = nullptr;
+  ClipIn ci{nullptr, 0, clip_norm};
   if (clip_norm > 0.f) {
     // the global L2 norm over every projection this step updates (the
     // reference clips all of its L*3 deltas together, grafting.hip:1149-1164;
@@ -248,13 +289,17 @@ static glt_status graft_step(const glt_graft_slice* slices, int32_t n_slices, fl
       }
     }
     if (segs.nseg > 0) {
-      glt_status s = launch_clip(segs, clip_norm, clip_ws, st);
+      glt_status s = launch_clip(segs, clip_ws, clip_ws_floats, &ci.np, st);
       if (s != GLT_OK) return s;
-      scale = clip_ws + kClipBlocks;
+      ci.partial = clip_ws;
     }
   }
   const float b1c = 1.0f / (1.0f - powf(beta1, (float)(step + 1)));
   const float b2c = 1.0f / (1.0f - powf(beta2, (float)(step + 1)));
+  // projections with whole 64 x 64 tiles and a packed mirror: one fused
+  // launch for all of them; the others one flat update and a repack each
+  PackJobs jobs{};
+  int tiles = 0;
   for (int j = 0; j < n_slices; ++j) {
     const glt_graft_slice& sl = slices[j];
     const int64_t sh = (int64_t)sl.s * sl.h;
@@ -267,23 +312,27 @@ static glt_status graft_step(const glt_graft_slice* slices, int32_t n_slices, fl
       float* vp = v[j] + p * sh;
       uint16_t* pk = packed_out ? packed_out[j] : nullptr;
       if (pk && sl.s % 64 == 0 && sl.h % 64 == 0 && al16(w) && al16(gp) && al16(mp) && al16(vp) && al16(pk)) {
-        const int64_t tiles = sh / 4096;
-        GLT_CHECK(tiles < (1ll << 31), GLT_ERR_SHAPE, "glt_adamw_graft_step: %lld tiles", (long long)tiles);
+        const int64_t t = sh / 4096;
+        GLT_CHECK(tiles + t < (1ll << 31), GLT_ERR_SHAPE, "glt_adamw_graft_step: %lld tiles", (long long)(tiles + t));
         uint16_t* rm = pk + 2 * p * sh;
-        GLT_LAUNCH("adamw_pack", adamw_pack_kernel, dim3((unsigned)tiles), dim3(256), 0, st, w, gp, mp, vp,
-                   sl.s, sl.h, lr, beta1, beta2, b1c, b2c, eps, weight_decay, scale, rm, rm + sh,
-                   pk + packed_shuf_offset(sl.s, sl.h, 2 * p), pk + packed_shuf_offset(sl.s, sl.h, 2 * p + 1));
-        GLT_LAUNCH_CHECK("adamw_pack");
+        jobs.j[jobs.n++] = PackJob{w, gp, mp, vp, rm, rm + sh, pk + packed_shuf_offset(sl.s, sl.h, 2 * p),
+                                   pk + packed_shuf_offset(sl.s, sl.h, 2 * p + 1), sl.s, sl.h, tiles};
+        tiles += (int)t;
         continue;
       }
       GLT_LAUNCH("adamw", adamw_kernel, dim3(grid_n(sh)), dim3(256), 0, st, w, gp, mp, vp, (uint16_t*)nullptr, sh,
-                 lr, beta1, beta2, b1c, b2c, eps, weight_decay, scale);
+                 lr, beta1, beta2, b1c, b2c, eps, weight_decay, ci);
       GLT_LAUNCH_CHECK("adamw_graft");
       if (pk) {
         glt_status s = pack_projection(w, sl.s, sl.h, p, pk, st);
         if (s != GLT_OK) return s;
       }
     }
+  }
+  if (jobs.n > 0) {
+    GLT_LAUNCH("adamw_pack", adamw_pack_kernel, dim3((unsigned)tiles), dim3(256), 0, st, jobs, lr, beta1, beta2, b1c,
+               b2c, eps, weight_decay, ci);
+    GLT_LAUNCH_CHECK("adamw_pack");
   }
   return GLT_OK;
 }
@@ -297,7 +346,7 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
   GLT_CHECK(clip_norm <= 0.f || (ws && ws_bytes >= glt_adamw_workspace_size(0)), GLT_ERR_WORKSPACE,
             "glt_adamw_graft_step: clip needs %zu workspace bytes", glt_adamw_workspace_size(0));
   return graft_step(slices, n_slices, grads, m, v, packed_out, proj_mask, step, lr, beta1, beta2, eps, weight_decay,
-                    clip_norm, static_cast<float*>(ws), as_stream(stream));
+                    clip_norm, static_cast<float*>(ws), ws_bytes / sizeof(float), as_stream(stream));
 }
 
 }  // extern "C"
