@@ -132,6 +132,9 @@ SIGNATURES = {
     "glt_adamw_graft_step": (_i32, [ctypes.POINTER(GraftSlice), _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                     ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i32, _i32, _f32, _f32, _f32, _f32,
                                     _f32, _f32, _vp, _sz, _vp]),
+    "glt_adamw_graft_step_noalloc": (_i32, [ctypes.POINTER(GraftSlice), _i32, ctypes.POINTER(_vp),
+                                            ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i32, _i32,
+                                            _f32, _f32, _f32, _f32, _f32, _f32, _vp]),
     "glt_shadow_bake": (_i32, [ctypes.POINTER(BakeDesc), ctypes.POINTER(ModelState), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                ctypes.POINTER(_vp), _vp]),

@@ -2,6 +2,7 @@
 // the bf16 mirror refresh fused into the update.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "common.hpp"
 #include "layout.hpp"
@@ -347,6 +348,53 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
             "glt_adamw_graft_step: clip needs %zu workspace bytes", glt_adamw_workspace_size(0));
   return graft_step(slices, n_slices, grads, m, v, packed_out, proj_mask, step, lr, beta1, beta2, eps, weight_decay,
                     clip_norm, static_cast<float*>(ws), ws_bytes / sizeof(float), as_stream(stream));
+}
+
+}  // extern "C"
+
+// ------------------------------------------------- the allocation-free step
+// glt_adamw_graft_step_noalloc keeps its clip partials in `scratch`, a
+// file-scope device array of kClipBlocks floats (4 KB) that every GPU the
+// library runs on holds until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol):
+// the device address of each GPU's copy is looked up once per device with
+// that device current and kept in g_scratch_ptr.
+namespace glt {
+static __device__ __align__(256) float scratch[kClipBlocks];
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[64] = {};  // per device, guarded by g_scratch_mu
+
+static glt_status scratch_ptr(float** out) {
+  int dev = 0;
+  GLT_TRY_HIP(hipGetDevice(&dev));
+  GLT_CHECK(dev >= 0 && dev < 64, GLT_ERR_HIP, "glt_adamw_graft_step_noalloc: device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    GLT_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    GLT_CHECK(p, GLT_ERR_HIP, "glt_adamw_graft_step_noalloc: no device address for the clip scratch");
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return GLT_OK;
+}
+}  // namespace glt
+
+extern "C" {
+
+glt_status glt_adamw_graft_step_noalloc(const glt_graft_slice* slices, int32_t n_slices, float* const* grads,
+                                        float* const* m, float* const* v, uint16_t* const* packed_out,
+                                        int32_t proj_mask, int32_t step, float lr, float beta1, float beta2,
+                                        float eps, float weight_decay, float clip_norm, void* stream) {
+  float* ws = nullptr;
+  if (clip_norm > 0.f) {
+    const glt_status s = scratch_ptr(&ws);
+    if (s != GLT_OK) return s;
+  }
+  // every partial the clip reads is written by the same call's sumsq launch,
+  // so the scratch needs no clearing
+  return graft_step(slices, n_slices, grads, m, v, packed_out, proj_mask, step, lr, beta1, beta2, eps, weight_decay,
+                    clip_norm, ws, ws ? (size_t)kClipBlocks : 0, as_stream(stream));
 }
 
 }  // extern "C"

@@ -1,0 +1,70 @@
+"""The allocation-free graft AdamW step (glt_adamw_graft_step_noalloc),
+called through the C ABI, against the workspace form glt_adamw_graft_step on
+identical state: masters, moments and the packed bf16 mirrors bit for bit,
+over two calls in a row (the second smaller, with a tighter clip, so its
+clip reads fewer partial sums than the first left in the library's array)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from helpers import draw
+
+pytestmark = pytest.mark.gpu
+
+
+def _state(torch, ops, shapes, seed):
+    slices, grads, ms, vs = [], [], [], []
+    for j, (S, H) in enumerate(shapes):
+        masters = [torch.from_numpy(draw((S, H), seed + j, p, 0, 0.02, bf16=False)).cuda() for p in range(3)]
+        slices.append(ops.GraftSlice(0, S, 0, H, *masters).pack())
+        grads.append(torch.from_numpy(draw((3 * S * H,), seed + 10 + j, 1, 0, 0.05, bf16=False)).cuda())
+        ms.append(torch.from_numpy(draw((3 * S * H,), seed + 20 + j, 1, 0, 1e-3, bf16=False)).cuda())
+        vs.append(torch.from_numpy(np.abs(draw((3 * S * H,), seed + 30 + j, 1, 0, 1e-4, bf16=False))).cuda())
+    return slices, grads, ms, vs
+
+
+def _clone(torch, ops, st):
+    slices, grads, ms, vs = st
+    out = []
+    for sl in slices:
+        c = ops.GraftSlice(sl.i_start, sl.s, sl.h_start, sl.h, sl.gate.clone(), sl.up.clone(), sl.down.clone())
+        c.packed.copy_(sl.packed)
+        out.append(c)
+    return out, [g.clone() for g in grads], [t.clone() for t in ms], [t.clone() for t in vs]
+
+
+def _call(F, ops, name, st, step, clip, extra):
+    slices, grads, ms, vs = st
+    arr = ops._slices_array(slices)
+    F.call(name, arr, len(slices), F.ptr_array([g.data_ptr() for g in grads]), F.ptr_array([t.data_ptr() for t in ms]),
+           F.ptr_array([t.data_ptr() for t in vs]), F.ptr_array([s.packed.data_ptr() for s in slices]), 7, step,
+           1e-3, 0.9, 0.999, 1e-8, 0.01, clip, *extra, ops._stream())
+
+
+def test_noalloc_graft_step_matches_workspace_form(dev):
+    import torch
+    from glt_amd import _ffi as F
+    from glt_amd import ops
+    ws_bytes = F.load().glt_adamw_workspace_size(0)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    for shapes, seed, step, clip in (([(128, 256), (64, 96)], 40, 3, 1.0),   # fused tiles + separate passes
+                                     ([(64, 128)], 60, 4, 0.25)):              # smaller, tighter clip
+        print("noalloc call", shapes, clip, flush=True)
+        a = _state(torch, ops, shapes, seed)
+        b = _clone(torch, ops, a)
+        _call(F, ops, "glt_adamw_graft_step", a, step, clip, (ctypes.c_void_p(ws.data_ptr()), ws_bytes))
+        _call(F, ops, "glt_adamw_graft_step_noalloc", b, step, clip, ())
+        torch.cuda.synchronize()
+        bits = lambda t: t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)
+        for sa, sb in zip(a[0], b[0]):
+            for x, y in ((sa.gate, sb.gate), (sa.up, sb.up), (sa.down, sb.down), (sa.packed, sb.packed)):
+                assert torch.equal(bits(x), bits(y))
+        for xs, ys in ((a[2], b[2]), (a[3], b[3])):
+            for x, y in zip(xs, ys):
+                assert torch.equal(bits(x), bits(y))
+        # the clip acted (the moments differ from an unclipped step)
+        c = _clone(torch, ops, _state(torch, ops, shapes, seed))
+        _call(F, ops, "glt_adamw_graft_step", c, step, 0.0, (None, 0))
+        torch.cuda.synchronize()
+        assert not torch.equal(c[2][0], b[2][0])
