@@ -4,14 +4,16 @@ Workload (one step): the Llama-3-8B-shape grafted MLP layer with bf16
 weights/activations and fp32 accumulation -- hidden 4096, base intermediate
 14336, one appended graft slice of 1024 neurons, 8 x 2048 = 16384 tokens --
     RMSNorm fwd (eps 1e-5) -> grafted MLP fwd -> graft-only MLP bwd (dX and
-    per-slice dW) -> RMSNorm bwd -> AdamW on the graft params (lr 1e-4,
-    betas 0.9/0.999, wd 0.01, no clip).
+    per-slice dW) from an f32 upstream gradient -> RMSNorm bwd -> AdamW on
+    the graft params (lr 1e-4, betas 0.9/0.999, wd 0.01, global clip 1.0).
 Inputs are synthetic (weights ~N(0,0.02), x ~N(0,1), gamma ~1+N(0,0.02),
-dy ~N(0,1)), drawn on the GPU and resident in HBM before timing.
+dy ~N(0,1) in f32 as the reference's backward receives it), drawn on the GPU
+and resident in HBM before timing.
 
 Also measured: shadow_bake materialising 32 layers of baked [15360,4096] /
-[4096,15360] matrices (GB/s against HBM), and the oracle (C restatement of
-the reference path) on a bounded token sample on the host cores.
+[4096,15360] matrices (GB/s against HBM), the HBM-bound kernels, attention
+and the decoder layer, and the reference's graft math in PyTorch on a bounded
+token sample on the host cores (cpu_baseline).
 
 Prints ONE JSON line. Usage: python bench.py [--steps K] [--warmup W]
 """
@@ -103,7 +105,7 @@ def main():
     log("[bench] drawing inputs")
     x_raw = fill(torch.empty((M, D), dtype=bf, device=dev), synth.SEED_X, synth.TID_X, 0.0, 1.0)
     gamma = fill(torch.empty(D, dtype=bf, device=dev), synth.SEED_GAMMA, synth.TID_GAMMA, 1.0, 0.02)
-    dy = fill(torch.empty((M, D), dtype=bf, device=dev), synth.SEED_DY, synth.TID_DY, 0.0, 1.0)
+    dy = fill(torch.empty((M, D), dtype=torch.float32, device=dev), synth.SEED_DY, synth.TID_DY, 0.0, 1.0)
     wg = fill(torch.empty((I, D), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_GATE, 0.0, 0.02)
     wu = fill(torch.empty((I, D), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_UP, 0.0, 0.02)
     wd = fill(torch.empty((D, I), dtype=bf, device=dev), synth.SEED_BASE, synth.TID_DOWN, 0.0, 0.02)
@@ -113,7 +115,7 @@ def main():
     sl = (F.GraftSlice * 1)()
     sl[0] = F.GraftSlice(I, S, 0, D, masters.data_ptr(), masters.data_ptr() + 4 * S * D,
                          masters.data_ptr() + 8 * S * D, packed.data_ptr())
-    desc = F.MlpDesc(M, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT, 1, sl, None)
+    desc = F.MlpDesc(M, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT | F.MLP_DY_F32, 1, sl, None)
     prepared = torch.empty(lib.glt_base_prepared_size(ctypes.byref(desc)), dtype=torch.uint8, device=dev)
     F.call("glt_base_prepare", ctypes.byref(desc), p(wg), p(wu), p(wd), p(prepared), sp)
     F.call("glt_graft_pack", sl, p(packed), sp)
@@ -203,19 +205,43 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                 "traffic_source": traffic_source, "flop_per_launch": dom_flop}
 
-    # HBM-bound kernels against the HBM roofline: RMSNorm and AdamW of the
-    # step, RoPE at the decoder-layer shape (2 x 4096 tokens, 32 q / 8 kv
-    # heads of 128, theta 5e5)
+    # HBM-bound kernels against the HBM roofline. RMSNorm, the clip and the
+    # AdamW update: their launches in the step above, each bracketed by HIP
+    # events on the launch stream (so in the step's own cache state; the
+    # bracket adds about a microsecond). RoPE at the decoder-layer shape
+    # (2 x 4096 tokens, 32 q / 8 kv heads of 128, theta 5e5): one launch at a
+    # time, after a read of a 1 GiB buffer that leaves none of its inputs in
+    # the caches (the 256 MB last-level cache would otherwise hold the whole
+    # input across repeated launches).
     hbm = {}
     for k, nbytes in HBM_BYTES.items():
         if k in kernels:
             t = kernels[k]["avg_ms"]
             hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
-                      "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
-    hbm["rope"] = bench_rope(torch, F, sp, p)
+                      "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "timing": "in the step"}
+    flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    flush_buf.fill_(1.0)
+    flush_out = torch.empty(1, dtype=torch.float32, device=dev)
+
+    def cold_ms(fn, reps=20):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        tot = 0.0
+        for _ in range(reps):
+            torch.sum(flush_buf, 0, out=flush_out)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            e1.synchronize()
+            tot += e0.elapsed_time(e1)
+        return tot / reps
+
+    hbm["rope"] = bench_rope(torch, F, sp, p, cold_ms)
     hbm["masked_ce"] = bench_masked_ce(torch, F, sp, p)
     hbm["eval_stats"] = bench_eval_stats(torch, F, sp, p)
     hbm["torch_copy"] = bench_copy(torch)
+    del flush_buf, flush_out
     attention = bench_attention(torch, F, sp, p)
     layer = None
     if not args.no_layer:
@@ -243,7 +269,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "Llama-3-8B-shape grafted SwiGLU MLP layer: RMSNorm + graft-only fwd+bwd + AdamW",
+        "config": {"workload": "Llama-3-8B-shape grafted SwiGLU MLP layer: RMSNorm + graft-only fwd+bwd (f32 upstream gradient) + clipped AdamW",
                    "tokens": M, "hidden": D, "base_intermediate": I, "graft_slice": S, "parallelism": "none (1 GPU)"},
         "step_mfma_frac": round(STEP_FLOP / (ms_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "gemm_mfma_frac": round(STEP_FLOP / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
@@ -259,7 +285,7 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def bench_rope(torch, F, sp, p, reps=20):
+def bench_rope(torch, F, sp, p, cold_ms):
     """RoPE in place on q [2,4096,32*128] and k [2,4096,8*128] bf16 (the
     decoder-layer shape); algorithmic bytes: q and k read and written."""
     bf = torch.bfloat16
@@ -271,18 +297,11 @@ def bench_rope(torch, F, sp, p, reps=20):
     def run():
         F.call("glt_rope_fwd", p(q), ROPE_HQ, p(k), ROPE_HK, ROPE_B, ROPE_T, ROPE_HD, ROPE_THETA, 0, sp)
 
-    run()
-    torch.cuda.synchronize()
-    F.call("glt_profile_enable", 1)
-    for _ in range(reps):
-        run()
-    torch.cuda.synchronize()
-    tot, cnt = F.profile_collect().get("rope", (0.0, 1))
-    F.call("glt_profile_enable", 0)
-    t = tot / cnt
+    t = cold_ms(run)
     nbytes = 2 * 2 * ROPE_B * ROPE_T * (ROPE_HQ + ROPE_HK) * ROPE_HD
     return {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
-            "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+            "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "timing": "one launch after a 1 GiB read, events around it"}
 
 
 def bench_eval_stats(torch, F, sp, p, reps=3):
@@ -401,7 +420,7 @@ def bench_layer(torch, F, lib, dev, sp, p, fill, base, sl, reps=5):
     ln_in = fill(torch.empty(D, dtype=bf, device=dev), 600, 5, 1.0, 0.02)
     ln_post = fill(torch.empty(D, dtype=bf, device=dev), 600, 6, 1.0, 0.02)
     x = fill(torch.empty((Mt, D), dtype=bf, device=dev), 600, 7, 0.0, 1.0)
-    dy = fill(torch.empty((Mt, D), dtype=bf, device=dev), 600, 8, 0.0, 1.0)
+    dy = fill(torch.empty((Mt, D), dtype=torch.float32, device=dev), 600, 8, 0.0, 1.0)
     md = F.MlpDesc(Mt, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT, 1, sl, None)
     ld = F.LayerDesc(B, T, ROPE_HQ, ROPE_HK, ROPE_HD, ROPE_THETA, EPS, md)
     lw = F.LayerWeights(p(wq), p(wk), p(wv), p(wo), p(ln_in), p(ln_post), None, base)
@@ -411,7 +430,7 @@ def bench_layer(torch, F, lib, dev, sp, p, fill, base, sl, reps=5):
     fws = torch.empty(lib.glt_layer_fwd_workspace_size(ctypes.byref(ld)), dtype=torch.uint8, device=dev)
     x_ffn = torch.empty_like(x)
     var = torch.empty(Mt, dtype=torch.float32, device=dev)
-    bd = F.MlpDesc(Mt, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT | F.MLP_RECOMPUTE, 1, sl, None)
+    bd = F.MlpDesc(Mt, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT | F.MLP_RECOMPUTE | F.MLP_DY_F32, 1, sl, None)
     bws = torch.empty(lib.glt_mlp_bwd_workspace_size(ctypes.byref(bd)), dtype=torch.uint8, device=dev)
     grads = torch.zeros(3 * S * D, dtype=torch.float32, device=dev)
     gg = (F.GraftGrads * 1)()

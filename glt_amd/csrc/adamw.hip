@@ -32,13 +32,22 @@ __global__ void __launch_bounds__(256) sumsq_partial_kernel(const ClipSegs segs,
     const int64_t n = segs.n[j];
     int64_t done = 0;
     if ((reinterpret_cast<uintptr_t>(g) & 15) == 0) {
-      // 16-byte loads over the whole multiple-of-4 prefix
+      // 16-byte loads over the whole multiple-of-4 prefix, four in flight
       const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
-      for (int64_t i = first; i < n / 4; i += stride) {
+      const int64_t n4 = n / 4;
+      int64_t i = first;
+      for (; i + 3 * stride < n4; i += 4 * stride) {
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = g4[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+      }
+      for (; i < n4; i += stride) {
         const f32x4 v = g4[i];
         s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
       }
-      done = n / 4 * 4;
+      done = n4 * 4;
     }
     for (int64_t i = done + first; i < n; i += stride) s += g[i] * g[i];
   }
@@ -160,7 +169,8 @@ __global__ void __launch_bounds__(256) adamw_pack_kernel(const PackJobs jobs, fl
     for (int i = 0; i < 4; ++i) {
       const int r = rr + 16 * i;
       const int64_t o = (int64_t)(r0 + r) * H + c0 + c4;
-      const f32x4 wi = *reinterpret_cast<const f32x4*>(w + o), gi = *reinterpret_cast<const f32x4*>(g + o);
+      const f32x4 wi = *reinterpret_cast<const f32x4*>(w + o);
+      const f32x4 gi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g + o));
       f32x4 mi = *reinterpret_cast<const f32x4*>(m + o), vi = *reinterpret_cast<const f32x4*>(v + o);
       f32x4 nw;
 #pragma unroll
@@ -171,9 +181,11 @@ __global__ void __launch_bounds__(256) adamw_pack_kernel(const PackJobs jobs, fl
         vi[e] = b;
         tile[r][c4 + e] = nw[e];
       }
-      *reinterpret_cast<f32x4*>(m + o) = mi;
-      *reinterpret_cast<f32x4*>(v + o) = vi;
-      *reinterpret_cast<f32x4*>(w + o) = nw;
+      // the moments and masters are read again only by the next step's
+      // update: written past the caches
+      __builtin_nontemporal_store(mi, reinterpret_cast<f32x4*>(m + o));
+      __builtin_nontemporal_store(vi, reinterpret_cast<f32x4*>(v + o));
+      __builtin_nontemporal_store(nw, reinterpret_cast<f32x4*>(w + o));
       u32x2 q;
       q.x = pack_bf16x2(nw[0], nw[1]);
       q.y = pack_bf16x2(nw[2], nw[3]);

@@ -79,10 +79,14 @@ __global__ void __launch_bounds__(256) shuffle_kernel(const TS* __restrict__ src
 // n0 + 8 cb + c holding K = k0 + 8 kb .. +7, which is chunk (substep kb/2,
 // lane (8 cb + c) % 32 + 32 (kb & 1)) of its block. The chunks go to their
 // place in the wavefront's 8 KB of LDS and leave as contiguous 1 KB stores.
+// SRC1_F32: the second source is f32; its 8 x 8 sub-blocks are rounded to
+// bf16 (RNE) on load and also written row-major to rm1 (the bf16 copy the
+// other GEMMs read), so one pass converts and lays out an f32 gradient.
+template <bool SRC1_F32>
 __global__ void __launch_bounds__(256) shuffle_tr16_kernel(const uint16_t* __restrict__ src0,
-                                                           const uint16_t* __restrict__ src1, int64_t ld, int rows,
+                                                           const void* __restrict__ src1, int64_t ld, int rows,
                                                            int K, int njobs, uint16_t* __restrict__ dst0,
-                                                           uint16_t* __restrict__ dst1) {
+                                                           uint16_t* __restrict__ dst1, uint16_t* __restrict__ rm1) {
   __shared__ __attribute__((aligned(16))) uint16_t stage[4][2 * kShufBlock];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int64_t tile = (int64_t)blockIdx.x * 4 + wave;
@@ -91,15 +95,26 @@ __global__ void __launch_bounds__(256) shuffle_tr16_kernel(const uint16_t* __res
   if (tile >= per * njobs) return;
   const bool second = tile >= per;
   if (second) tile -= per;
-  const uint16_t* __restrict__ src = second ? src1 : src0;
   uint16_t* __restrict__ dst = second ? dst1 : dst0;
   const int nt = (int)(tile / kt), ktile = (int)(tile % kt);
   const int n0 = nt * 64, k0 = ktile * 64;
   const int cb = lane & 7, kb = lane >> 3;
   u32x4 in[8];
+  if (SRC1_F32 && second) {
+    const float* __restrict__ src = static_cast<const float*>(src1);
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
-    in[r] = *reinterpret_cast<const u32x4*>(src + (int64_t)(k0 + 8 * kb + r) * ld + n0 + 8 * cb);
+    for (int r = 0; r < 8; ++r) {
+      const int64_t o = (int64_t)(k0 + 8 * kb + r) * ld + n0 + 8 * cb;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(src + o), b = *reinterpret_cast<const f32x4*>(src + o + 4);
+      in[r] = u32x4{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)};
+      *reinterpret_cast<u32x4*>(rm1 + o) = in[r];
+    }
+  } else {
+    const uint16_t* __restrict__ src = second ? static_cast<const uint16_t*>(src1) : src0;
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      in[r] = *reinterpret_cast<const u32x4*>(src + (int64_t)(k0 + 8 * kb + r) * ld + n0 + 8 * cb);
+  }
   uint16_t* st = stage[wave];
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
@@ -138,8 +153,27 @@ glt_status shuffle_b_tr_pair(const void* src0, const void* src1, int src_dtype, 
   }
   const int64_t tiles = 2 * (int64_t)(rows / 64) * (K / 64);
   GLT_CHECK(tiles < (1ll << 33), GLT_ERR_SHAPE, "shuffle_b_tr_pair: %lld tiles", (long long)tiles);
-  GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st,
-             static_cast<const uint16_t*>(src0), static_cast<const uint16_t*>(src1), ld, rows, K, 2, dst0, dst1);
+  GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel<false>, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st,
+             static_cast<const uint16_t*>(src0), src1, ld, rows, K, 2, dst0, dst1, (uint16_t*)nullptr);
+  GLT_LAUNCH_CHECK("shuffle_tr");
+  return GLT_OK;
+}
+
+bool shuffle_tr_pair_f32_ok(const void* src0, const float* src1, int64_t ld, int rows, int K, const void* dst0,
+                            const void* dst1, const void* rm1) {
+  return rows > 0 && K > 0 && rows % 64 == 0 && K % 64 == 0 && ld % 8 == 0 && src0 && src1 && dst0 && dst1 && rm1 &&
+         ((reinterpret_cast<uintptr_t>(src0) | reinterpret_cast<uintptr_t>(src1) | reinterpret_cast<uintptr_t>(dst0) |
+           reinterpret_cast<uintptr_t>(dst1) | reinterpret_cast<uintptr_t>(rm1)) & 15) == 0;
+}
+
+glt_status shuffle_tr_pair_f32(const uint16_t* src0, const float* src1, int64_t ld, int rows, int K, uint16_t* dst0,
+                               uint16_t* dst1, uint16_t* rm1, hipStream_t st) {
+  GLT_CHECK(shuffle_tr_pair_f32_ok(src0, src1, ld, rows, K, dst0, dst1, rm1), GLT_ERR_UNSUPPORTED,
+            "shuffle_tr_pair_f32: shape or alignment");
+  const int64_t tiles = 2 * (int64_t)(rows / 64) * (K / 64);
+  GLT_CHECK(tiles < (1ll << 33), GLT_ERR_SHAPE, "shuffle_tr_pair_f32: %lld tiles", (long long)tiles);
+  GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel<true>, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, src0,
+             static_cast<const void*>(src1), ld, rows, K, 2, dst0, dst1, rm1);
   GLT_LAUNCH_CHECK("shuffle_tr");
   return GLT_OK;
 }
@@ -162,8 +196,8 @@ glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed
     if (transposed && rows % 64 == 0 && K % 64 == 0 && ld % 8 == 0 &&
         ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
       const int64_t tiles = (int64_t)(rows / 64) * (K / 64);
-      GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, s, s, ld, rows,
-                 K, 1, dst, dst);
+      GLT_LAUNCH("shuffle_tr", shuffle_tr16_kernel<false>, dim3((unsigned)cdiv(tiles, 4)), dim3(256), 0, st, s,
+                 static_cast<const void*>(s), ld, rows, K, 1, dst, dst, (uint16_t*)nullptr);
       GLT_LAUNCH_CHECK("shuffle_tr");
       return GLT_OK;
     }

@@ -69,6 +69,13 @@ glt_status shuffle_b_tr_pair(const void* src0, const void* src1, int src_dtype, 
                             uint16_t* dst0, uint16_t* dst1, hipStream_t st);
 glt_status shuffle_b(const void* src, int src_dtype, int64_t ld, bool transposed, int rows, int K, uint16_t* dst,
                      hipStream_t st);
+// shuffle_b_tr_pair for a bf16 src0 and an f32 src1 (whole 64 x 64 tiles,
+// 16-byte aligned): src1 is rounded to bf16 (RNE) and its row-major bf16
+// copy is written to rm1 in the same pass.
+bool shuffle_tr_pair_f32_ok(const void* src0, const float* src1, int64_t ld, int rows, int K, const void* dst0,
+                            const void* dst1, const void* rm1);
+glt_status shuffle_tr_pair_f32(const uint16_t* src0, const float* src1, int64_t ld, int rows, int K, uint16_t* dst0,
+                               uint16_t* dst1, uint16_t* rm1, hipStream_t st);
 
 // out[i] = RNE bf16 of in[i].
 glt_status convert_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st);

@@ -274,14 +274,27 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
   void* dg = W + L.dg;
   void* du = W + L.du;
 
+  const bool grads_wanted = explicit_graft && d->n_slices > 0;
+  bool operands_laid_out = false;  // x and dy already in the weight-gradient fragment layout
   if (L.dy_f32) {
     // The reference multiplies its f32 upstream gradient by the f32 copy of
     // W_down (src/layer_backward_impl.inc:48) and rounds it to bf16 for the
     // graft GEMMs (src/gemm_impl.inc:454-455, :524-525). The MFMA operands
     // are bf16, so the gradient is rounded once (RNE) here and every GEMM
-    // below reads that copy.
+    // below reads that copy; when the weight gradients need x and dy in the
+    // fragment layout, the same pass writes them.
     uint16_t* dyb = reinterpret_cast<uint16_t*>(W + L.dyb);
-    if ((s = convert_f32_to_bf16(static_cast<const float*>(dy), dyb, (int64_t)d->M * d->D, st)) != GLT_OK) return s;
+    const float* dyf = static_cast<const float*>(dy);
+    uint16_t* XS = reinterpret_cast<uint16_t*>(W + L.xt);
+    uint16_t* DYS = reinterpret_cast<uint16_t*>(W + L.dyt);
+    if (L.wgrad_mfma && grads_wanted && shuffle_tr_pair_f32_ok(x, dyf, d->D, d->D, d->M, XS, DYS, dyb)) {
+      if ((s = shuffle_tr_pair_f32(static_cast<const uint16_t*>(x), dyf, d->D, d->D, d->M, XS, DYS, dyb, st)) !=
+          GLT_OK)
+        return s;
+      operands_laid_out = true;
+    } else if ((s = convert_f32_to_bf16(dyf, dyb, (int64_t)d->M * d->D, st)) != GLT_OK) {
+      return s;
+    }
     dy = dyb;
   }
 
@@ -368,7 +381,7 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
     // B operands [D rows, K = M] once for all slices.
     uint16_t* XS = reinterpret_cast<uint16_t*>(W + L.xt);
     uint16_t* DYS = reinterpret_cast<uint16_t*>(W + L.dyt);
-    if ((s = shuffle_b_tr_pair(x, dy, dt, D, D, M, XS, DYS, st)) != GLT_OK) return s;
+    if (!operands_laid_out && (s = shuffle_b_tr_pair(x, dy, dt, D, D, M, XS, DYS, st)) != GLT_OK) return s;
     const size_t es = esize(dt);
     // every slice transpose first, batched into few launches
     {

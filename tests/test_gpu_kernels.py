@@ -228,7 +228,7 @@ def test_rmsnorm(dev, M, D):
 
 
 # ------------------------------------------------------------------- RoPE
-@pytest.mark.parametrize("hd,pos0", [(128, 0), (64, 17)])
+@pytest.mark.parametrize("hd,pos0", [(128, 0), (64, 17), (40, 5)])   # 40: the element-wise kernel
 def test_rope(dev, hd, pos0):
     import torch
     from glt_amd import ops
