@@ -275,12 +275,27 @@ struct EvalRow {
 constexpr uint64_t kFnvBasis = 1469598103934665603ULL;
 constexpr uint64_t kFnvPrime = 1099511628211ULL;  // 2^40 + 0x1B3
 
-// Every row is cut into kEvalChunks chunks of ceil(V / kEvalChunks) logits
-// (the last ones shorter or empty); one thread walks one chunk in order.
+// Row-hash form: every row is cut into kEvalChunks chunks of
+// ceil(V / kEvalChunks) logits (the last ones shorter or empty), which
+// defines that hash; one thread walks one chunk in order.
 constexpr int kEvalChunks = 16;
 
 __device__ __forceinline__ void chunk_range(int V, int c, int& v0, int& v1) {
   const int L = (V + kEvalChunks - 1) / kEvalChunks;
+  v0 = min(V, c * L);
+  v1 = min(V, v0 + L);
+}
+
+// The reference hash's passes cut every row into kHashChunks chunks of
+// ceil(V / kHashChunks) logits rounded up to a multiple of 8 (16-byte chunk
+// starts in rows that start on 16 bytes; the last chunks shorter or empty).
+// Any cut gives the same hash. (64 chunks per row, 4x the threads, measured
+// 2 % slower over the three passes at 16384 x 128256: the passes are bound
+// by their arithmetic, not by the chunk walks' load latency.)
+constexpr int kHashChunks = 16;
+
+__device__ __forceinline__ void hash_chunk_range(int V, int c, int& v0, int& v1) {
+  const int L = ((V + kHashChunks - 1) / kHashChunks + 7) & ~7;
   v0 = min(V, c * L);
   v1 = min(V, v0 + L);
 }
@@ -317,13 +332,12 @@ __device__ __forceinline__ void walk_chunk(const uint16_t* x, int v0, int v1, F&
   }
 }
 
-// One workgroup per 16 rows, 16 threads per row: thread c of a row takes
-// chunk c and accumulates its f64 sum and sum of squares, its maximum and
-// (ROW_HASH) the FNV-1a hash of the chunk's f32 bytes from the basis. The
+// Row-hash form: one workgroup per 16 rows, 16 threads per row: thread c of
+// a row takes chunk c and accumulates its f64 sum and sum of squares, its
+// maximum and the FNV-1a hash of the chunk's f32 bytes from the basis. The
 // row's threads then share their maxima through LDS, sum exp(x - max) over
 // their chunks, and thread 0 of the row adds the parts in chunk order and
-// (ROW_HASH) hashes the chunk hashes' little-endian bytes in order.
-template <bool ROW_HASH>
+// hashes the chunk hashes' little-endian bytes in order.
 __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, int64_t ld, const int32_t* ids, int B,
                                                         int T, int V, EvalRow* rows) {
   __shared__ float s_max[16][kEvalChunks], s_se[16][kEvalChunks];
@@ -345,12 +359,10 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
       s += f;
       s2 += (double)f * f;
       mx = fmaxf(mx, f);
-      if constexpr (ROW_HASH) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          h ^= (bits >> (8 * k)) & 0xFFu;
-          h *= kFnvPrime;
-        }
+      for (int k = 0; k < 4; ++k) {
+        h ^= (bits >> (8 * k)) & 0xFFu;
+        h *= kFnvPrime;
       }
     });
   s_max[lr][c] = mx;
@@ -374,12 +386,10 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
     o.sum += s_sum[lr][k];
     o.sumsq += s_sq[lr][k];
     tse += s_se[lr][k];
-    if constexpr (ROW_HASH) {
-      const uint64_t hk = s_h[lr][k];
-      for (int j = 0; j < 8; ++j) {
-        o.hash ^= (hk >> (8 * j)) & 0xFFu;
-        o.hash *= kFnvPrime;
-      }
+    const uint64_t hk = s_h[lr][k];
+    for (int j = 0; j < 8; ++j) {
+      o.hash ^= (hk >> (8 * j)) & 0xFFu;
+      o.hash *= kFnvPrime;
     }
   }
   if (scored) {
@@ -391,11 +401,110 @@ __global__ void __launch_bounds__(256) eval_rows_kernel(const uint16_t* logits, 
   rows[r] = o;
 }
 
+// (max, sum of exp(x - max)) pairs: the sum rescaled to the larger maximum
+__device__ __forceinline__ void lse_merge(float& m, float& se, float m2, float se2) {
+  const float M = fmaxf(m, m2);
+  se = se * __expf(m - M) + se2 * __expf(m2 - M);
+  m = M;
+}
+
+// Row statistics without the row hash (the reference hash runs in its own
+// passes): one workgroup per row reads it once with coalesced 16-byte loads.
+// Each thread keeps a running maximum m and the sum of exp(x - m), rescaled
+// when m grows (once per 8 logits at most), and f64 sums of x and x^2; the
+// threads' parts are merged by a butterfly in each wavefront and the four
+// wavefront results in order.
+__global__ void __launch_bounds__(256) eval_row_stats_kernel(const uint16_t* logits, int64_t ld, const int32_t* ids,
+                                                             int T, int V, EvalRow* rows) {
+  __shared__ float s_m[4], s_se[4];
+  __shared__ double s_s[4], s_q[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t r = blockIdx.x;
+  const uint16_t* x = logits + r * ld;
+  double s = 0.0, s2 = 0.0;
+  float m = -3.402823466e38f, se = 0.f;  // a finite start keeps exp(-inf - m) at 0
+  auto add8 = [&](const u32x4& q) {
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = __uint_as_float(q[e] << 16);
+      f[2 * e + 1] = __uint_as_float(q[e] & 0xFFFF0000u);
+    }
+    float lm = f[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) lm = fmaxf(lm, f[e]);
+    if (lm > m) {
+      se *= __expf(m - lm);
+      m = lm;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      se += __expf(f[e] - m);
+      s += (double)f[e];
+      s2 += (double)(f[e] * f[e]);  // exact: a bf16 square fits in f32
+    }
+  };
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && V % 8 == 0) {
+    const u32x4* xc = reinterpret_cast<const u32x4*>(x);
+    const int nc = V >> 3;
+    int c = tid;
+    for (; c + 768 < nc; c += 1024) {
+      u32x4 q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = __builtin_nontemporal_load(xc + c + 256 * u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) add8(q[u]);
+    }
+    for (; c < nc; c += 256) add8(__builtin_nontemporal_load(xc + c));
+  } else {
+    for (int v = tid; v < V; v += 256) {
+      const float f = __uint_as_float((uint32_t)x[v] << 16);
+      if (f > m) {
+        se *= __expf(m - f);
+        m = f;
+      }
+      se += __expf(f - m);
+      s += (double)f;
+      s2 += (double)(f * f);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lse_merge(m, se, __shfl_xor(m, o, 64), __shfl_xor(se, o, 64));
+    s += __shfl_xor(s, o, 64);
+    s2 += __shfl_xor(s2, o, 64);
+  }
+  if (lane == 0) {
+    s_m[tid >> 6] = m;
+    s_se[tid >> 6] = se;
+    s_s[tid >> 6] = s;
+    s_q[tid >> 6] = s2;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  EvalRow o{s_s[0], s_q[0], kFnvBasis, 0.f, 0};
+  float rmx = s_m[0], tse = s_se[0];
+  for (int k = 1; k < 4; ++k) {
+    o.sum += s_s[k];
+    o.sumsq += s_q[k];
+    lse_merge(rmx, tse, s_m[k], s_se[k]);
+  }
+  const int t = (int)(r % T);
+  if (t < T - 1) {
+    const int label = ids[r + 1];
+    const float xl = (label >= 0 && label < V) ? __uint_as_float((uint32_t)x[label] << 16) : NAN;
+    o.nll = (rmx + logf(tse)) - xl;
+    o.scored = 1;
+  }
+  rows[r] = o;
+}
+
 // ------------------------------------------------ the reference's logits hash
 // The reference hashes every f32 logit's four little-endian bytes in (b, t, v)
 // order with one FNV-1a chain, h = (h ^ byte) * P mod 2^64 (grafting.hip:536-546),
 // continued across its eval batches. That chain is computed here exactly, in
-// parallel over the chunks of all rows (chunk k = row k / 16, part k % 16),
+// parallel over the chunks of all rows (chunk k = row k / kHashChunks, part
+// k % kHashChunks),
 // in three passes:
 //  * P is odd, so the low byte of h evolves on its own:
 //    s' = ((s ^ byte) * P) mod 256. Bit j of s' depends only on bits 0..j of
@@ -418,28 +527,123 @@ __device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t k) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * (u16x2){(uint16_t)k, (uint16_t)k});
 }
 
-// Passes 1 and 2: 16 runs of the low-byte chain over chunk k, two per
-// register (16-bit halves; the low byte of a product depends only on the
-// operands' low bytes, so the high bytes may hold anything). PASS 0 starts
-// run i at nibble i and records the final low nibbles; PASS 1 starts run i
-// at (i << 4) | low nibble of the chunk and records the final high nibbles.
-// maps[k] nibble i = the final nibble of run i.
-template <int PASS>
-__global__ void __launch_bounds__(256) hash_nibble_kernel(const uint16_t* logits, int64_t ld, int64_t chunks, int V,
-                                                          const uint8_t* __restrict__ start_lo,
-                                                          uint64_t* __restrict__ maps) {
+// Pass 1 in bit planes. Per logit the low nibble goes
+//   s <- ((9 s ^ a) * 3 ^ b) * 3 mod 16   (P mod 16 = 3, a / b: low nibbles of lo / hi)
+// and the 16 runs of a chunk are kept as four 16-bit planes (bit i of plane
+// j = bit j of run i), two chunks of one row per thread in the two halves
+// of each 32-bit plane: 9 s flips bit 3 by bit 0, 3 s = s + 2 s is a ripple
+// carry over the planes, and XOR with a logit's bit is a XOR with that bit
+// spread over the chunk's half. About 19 operations per logit, against 40
+// for 16 runs held as 16-bit integers.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+struct Planes {
+  uint32_t p0, p1, p2, p3;
+};
+// bit k of each 16-bit half of w, spread over that half (0 or 0xFFFF)
+__device__ __forceinline__ uint32_t half_mask(uint32_t w, int k) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, w << (15 - k)) >> (s16x2){15, 15});
+}
+__device__ __forceinline__ void planes_x3(Planes& P) {
+  const uint32_t c1 = P.p1 & P.p0, t = P.p2 ^ P.p1;
+  const uint32_t c2 = (t & c1) | (~t & P.p2);  // carry into bit 3: majority of p2, p1, c1
+  P.p3 ^= P.p2 ^ c2;
+  P.p2 = t ^ c1;
+  P.p1 ^= P.p0;
+}
+// one logit of each chunk: chunk A's 16 bits in the low half of w, B's high
+__device__ __forceinline__ void planes_step(Planes& P, uint32_t w) {
+  P.p3 ^= P.p0 ^ half_mask(w, 3);  // 9 s, then ^ a
+  P.p0 ^= half_mask(w, 0);
+  P.p1 ^= half_mask(w, 1);
+  P.p2 ^= half_mask(w, 2);
+  planes_x3(P);
+  P.p0 ^= half_mask(w, 8);
+  P.p1 ^= half_mask(w, 9);
+  P.p2 ^= half_mask(w, 10);
+  P.p3 ^= half_mask(w, 11);
+  planes_x3(P);
+}
+// chunk pair kp = chunks 2 kp, 2 kp + 1 (the same row: kHashChunks is even);
+// the second one is never longer than the first
+static_assert(kHashChunks % 2 == 0, "chunk pairs share a row");
+__global__ void __launch_bounds__(256) hash_lo_planes_kernel(const uint16_t* logits, int64_t ld, int64_t chunks, int V,
+                                                             uint64_t* __restrict__ maps) {
+  const int64_t kA = 2 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+  if (kA >= chunks) return;
+  const uint16_t* x = logits + (kA / kHashChunks) * ld;
+  int a0, a1, b0, b1;
+  hash_chunk_range(V, (int)(kA & (kHashChunks - 1)), a0, a1);
+  hash_chunk_range(V, (int)((kA + 1) & (kHashChunks - 1)), b0, b1);
+  const int na = a1 - a0, nb = b1 - b0;
+  Planes P{0xAAAAAAAAu, 0xCCCCCCCCu, 0xF0F0F0F0u, 0xFF00FF00u};  // run i starts at nibble i
+  auto step2 = [&](uint32_t qa, uint32_t qb) {  // two logits of each chunk, in order
+    planes_step(P, (qa & 0xFFFFu) | (qb << 16));
+    planes_step(P, (qa >> 16) | (qb & 0xFFFF0000u));
+  };
+  int v = 0;
+  const bool vec = ((reinterpret_cast<uintptr_t>(x + a0) | reinterpret_cast<uintptr_t>(x + b0)) & 15) == 0;
+  if (vec) {
+    const u32x4* xa = reinterpret_cast<const u32x4*>(x + a0);
+    const u32x4* xb = reinterpret_cast<const u32x4*>(x + b0);
+    for (; v + 32 <= nb; v += 32) {
+      u32x4 qa[4], qb[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        qa[u] = xa[(v >> 3) + u];
+        qb[u] = xb[(v >> 3) + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) step2(qa[u][e], qb[u][e]);
+    }
+    for (; v + 8 <= nb; v += 8) {
+      const u32x4 qa = xa[v >> 3], qb = xb[v >> 3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) step2(qa[e], qb[e]);
+    }
+  }
+  for (; v < nb; ++v) planes_step(P, (uint32_t)x[a0 + v] | ((uint32_t)x[b0 + v] << 16));
+  // the rest of chunk A (B ran out): B's half of every plane is kept
+  for (; v < na; ++v) {
+    const Planes Q = P;
+    planes_step(P, (uint32_t)x[a0 + v]);
+    P.p0 = (P.p0 & 0xFFFFu) | (Q.p0 & 0xFFFF0000u);
+    P.p1 = (P.p1 & 0xFFFFu) | (Q.p1 & 0xFFFF0000u);
+    P.p2 = (P.p2 & 0xFFFFu) | (Q.p2 & 0xFFFF0000u);
+    P.p3 = (P.p3 & 0xFFFFu) | (Q.p3 & 0xFFFF0000u);
+  }
+  uint64_t mA = 0, mB = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t sa = ((P.p0 >> i) & 1u) | (((P.p1 >> i) & 1u) << 1) | (((P.p2 >> i) & 1u) << 2) |
+                        (((P.p3 >> i) & 1u) << 3);
+    const uint32_t sb = ((P.p0 >> (16 + i)) & 1u) | (((P.p1 >> (16 + i)) & 1u) << 1) |
+                        (((P.p2 >> (16 + i)) & 1u) << 2) | (((P.p3 >> (16 + i)) & 1u) << 3);
+    mA |= (uint64_t)sa << (4 * i);
+    mB |= (uint64_t)sb << (4 * i);
+  }
+  maps[kA] = mA;
+  maps[kA + 1] = mB;
+}
+
+// Pass 2: 16 runs of the low-byte chain over chunk k, two per register
+// (16-bit halves; the low byte of a product depends only on the operands'
+// low bytes, so the high bytes may hold anything), run i starting at
+// (i << 4) | the chunk's starting low nibble. maps[k] nibble i = the final
+// high nibble of run i.
+__global__ void __launch_bounds__(256) hash_hi_nibble_kernel(const uint16_t* logits, int64_t ld, int64_t chunks, int V,
+                                                             const uint8_t* __restrict__ start_lo,
+                                                             uint64_t* __restrict__ maps) {
   const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (k >= chunks) return;
-  const uint32_t base = PASS == 0 ? 0u : start_lo[k];
+  const uint32_t base = start_lo[k];
   uint32_t st[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t a = PASS == 0 ? 2 * i : (base | ((2 * i) << 4)), b = PASS == 0 ? 2 * i + 1 : (base | ((2 * i + 1) << 4));
-    st[i] = a | (b << 16);
-  }
+  for (int i = 0; i < 8; ++i) st[i] = (base | ((2 * i) << 4)) | ((base | ((2 * i + 1) << 4)) << 16);
   int v0, v1;
-  chunk_range(V, (int)(k & (kEvalChunks - 1)), v0, v1);
-  walk_chunk(logits + (k / kEvalChunks) * ld, v0, v1, [&](uint32_t w) {
+  hash_chunk_range(V, (int)(k & (kHashChunks - 1)), v0, v1);
+  walk_chunk(logits + (k / kHashChunks) * ld, v0, v1, [&](uint32_t w) {
     const uint32_t lo = (w & 0xFFu) * 0x10001u, hi = (w >> 8) * 0x10001u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) st[i] = pk_mul(pk_mul(pk_mul(st[i], kP16sq) ^ lo, kP16) ^ hi, kP16);
@@ -450,7 +654,7 @@ __global__ void __launch_bounds__(256) hash_nibble_kernel(const uint16_t* logits
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const uint32_t v = (st[i] >> (16 * hh)) & 0xFFu;
-      m |= (uint64_t)(PASS == 0 ? (v & 15u) : (v >> 4)) << (4 * (2 * i + hh));
+      m |= (uint64_t)(v >> 4) << (4 * (2 * i + hh));
     }
   maps[k] = m;
 }
@@ -486,12 +690,30 @@ __global__ void __launch_bounds__(256) nib_scan_up_kernel(const uint64_t* __rest
   if (t == 0) agg[blockIdx.x] = s[0];
 }
 
-// Step 2: the starting nibble of every workgroup, in order from `start`.
-__global__ void __launch_bounds__(64) nib_scan_top_kernel(const uint64_t* __restrict__ agg, int64_t nblocks,
-                                                          uint32_t start, uint8_t* __restrict__ bstart) {
-  if (threadIdx.x != 0) return;
-  uint32_t s = start;
-  for (int64_t b = 0; b < nblocks; ++b) {
+// Step 2: the starting nibble of every workgroup, in order from `start`:
+// each thread composes a run of consecutive workgroup maps, thread 0 walks
+// the 256 run maps, and each thread then walks its own run.
+__global__ void __launch_bounds__(256) nib_scan_top_kernel(const uint64_t* __restrict__ agg, int64_t nblocks,
+                                                           uint32_t start, uint8_t* __restrict__ bstart) {
+  __shared__ uint64_t run[256];
+  __shared__ uint8_t rs[256];
+  const int t = threadIdx.x;
+  const int64_t q = (nblocks + 255) / 256;
+  const int64_t b0 = min(nblocks, t * q), b1 = min(nblocks, b0 + q);
+  uint64_t f = kNibIdentity;
+  for (int64_t b = b0; b < b1; ++b) f = nib_compose(f, agg[b]);
+  run[t] = f;
+  __syncthreads();
+  if (t == 0) {
+    uint32_t s = start;
+    for (int i = 0; i < 256; ++i) {
+      rs[i] = (uint8_t)s;
+      s = nib_apply(run[i], s);
+    }
+  }
+  __syncthreads();
+  uint32_t s = rs[t];
+  for (int64_t b = b0; b < b1; ++b) {
     bstart[b] = (uint8_t)s;
     s = nib_apply(agg[b], s);
   }
@@ -551,10 +773,10 @@ __global__ void __launch_bounds__(256) hash_affine_kernel(const uint16_t* logits
   Affine f{1, 0};
   if (k < chunks) {
     int v0, v1;
-    chunk_range(V, (int)(k & (kEvalChunks - 1)), v0, v1);
+    hash_chunk_range(V, (int)(k & (kHashChunks - 1)), v0, v1);
     const uint64_t s0 = start_byte[k];
     uint64_t h = s0;
-    walk_chunk(logits + (k / kEvalChunks) * ld, v0, v1, [&](uint32_t w) {
+    walk_chunk(logits + (k / kHashChunks) * ld, v0, v1, [&](uint32_t w) {
       h = fnv_mul(fnv_mul(h));
       h = fnv_mul(h ^ (w & 0xFFu));
       h = fnv_mul(h ^ (w >> 8));
@@ -721,7 +943,7 @@ struct EvalWs {
 };
 EvalWs eval_ws(int64_t R) {
   EvalWs w{};
-  w.chunks = R * kEvalChunks;
+  w.chunks = R * kHashChunks;
   w.nscan = cdiv(w.chunks, kScanBlock);
   w.naff = cdiv(w.chunks, 256);
   w.rows = 0;
@@ -742,7 +964,7 @@ glt_status nib_scan(const EvalWs& w, char* ws, uint32_t start, bool high, hipStr
   uint8_t* out = reinterpret_cast<uint8_t*>(ws + w.start);
   GLT_LAUNCH("eval_hash_scan", nib_scan_up_kernel, dim3((unsigned)w.nscan), dim3(256), 0, st, maps, w.chunks, agg);
   GLT_LAUNCH_CHECK("nib_scan_up");
-  GLT_LAUNCH("eval_hash_scan", nib_scan_top_kernel, dim3(1), dim3(64), 0, st, agg, w.nscan, start, bstart);
+  GLT_LAUNCH("eval_hash_scan", nib_scan_top_kernel, dim3(1), dim3(256), 0, st, agg, w.nscan, start, bstart);
   GLT_LAUNCH_CHECK("nib_scan_top");
   if (high)
     GLT_LAUNCH("eval_hash_scan", nib_scan_down_kernel<4>, dim3((unsigned)w.nscan), dim3(256), 0, st, maps, w.chunks,
@@ -783,10 +1005,9 @@ glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids
   char* ws = static_cast<char*>(workspace);
   EvalRow* rows = reinterpret_cast<EvalRow*>(ws + w.rows);
   if (exact)
-    GLT_LAUNCH("eval_rows", eval_rows_kernel<false>, dim3((unsigned)((R + 15) / 16)), dim3(256), 0, st, logits, ld,
-               ids, B, T, V, rows);
+    GLT_LAUNCH("eval_rows", eval_row_stats_kernel, dim3((unsigned)R), dim3(256), 0, st, logits, ld, ids, T, V, rows);
   else
-    GLT_LAUNCH("eval_rows", eval_rows_kernel<true>, dim3((unsigned)((R + 15) / 16)), dim3(256), 0, st, logits, ld,
+    GLT_LAUNCH("eval_rows", eval_rows_kernel, dim3((unsigned)((R + 15) / 16)), dim3(256), 0, st, logits, ld,
                ids, B, T, V, rows);
   GLT_LAUNCH_CHECK("eval_rows");
   Affine* aff = reinterpret_cast<Affine*>(ws + w.aff);
@@ -794,12 +1015,12 @@ glt_status glt_eval_stats(const uint16_t* logits, int64_t ld, const int32_t* ids
     uint64_t* maps = reinterpret_cast<uint64_t*>(ws + w.maps);
     uint8_t* start = reinterpret_cast<uint8_t*>(ws + w.start);
     const dim3 grid((unsigned)w.naff);
-    GLT_LAUNCH("eval_hash_nibble", hash_nibble_kernel<0>, grid, dim3(256), 0, st, logits, ld, w.chunks, V,
-               (const uint8_t*)nullptr, maps);
+    GLT_LAUNCH("eval_hash_nibble", hash_lo_planes_kernel, dim3((unsigned)cdiv(w.chunks / 2, 256)), dim3(256), 0, st,
+               logits, ld, w.chunks, V, maps);
     GLT_LAUNCH_CHECK("hash_nibble");
     glt_status s = nib_scan(w, ws, (uint32_t)(hash_in & 15), false, st);
     if (s != GLT_OK) return s;
-    GLT_LAUNCH("eval_hash_nibble", hash_nibble_kernel<1>, grid, dim3(256), 0, st, logits, ld, w.chunks, V,
+    GLT_LAUNCH("eval_hash_nibble", hash_hi_nibble_kernel, grid, dim3(256), 0, st, logits, ld, w.chunks, V,
                (const uint8_t*)start, maps);
     GLT_LAUNCH_CHECK("hash_nibble");
     if ((s = nib_scan(w, ws, (uint32_t)((hash_in >> 4) & 15), true, st)) != GLT_OK) return s;
