@@ -55,6 +55,13 @@ HBM_BYTES = {
     "adamw_pack": 3 * S * D * (4 * 4 + 3 * 4 + 4 * 2),
     # the clip's sum of squares over the three projections' gradients
     "clip_sumsq": 3 * S * D * 4,
+    # the backward's operand layout pass: x (bf16) and the f32 upstream
+    # gradient in; the gradient rounded to bf16 (row-major) and x and the
+    # gradient transposed into the MFMA fragment layout out
+    "shuffle_tr": M * D * (2 + 4) + 3 * M * D * 2,
+    # the three graft slices of dgate, dup and inter transposed for the
+    # weight-gradient GEMMs (read and written once)
+    "transpose16": 3 * M * S * 2 * 2,
 }
 ROPE_B, ROPE_T, ROPE_HQ, ROPE_HK, ROPE_HD, ROPE_THETA = 2, 4096, 32, 8, 128, 500000.0
 # masked cross-entropy bench: 4 x 4096 tokens, Llama-3 vocabulary
@@ -75,6 +82,9 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the decoder-layer measurement")
     ap.add_argument("--layer-only", action="store_true",
                     help="only the attention kernel and decoder-layer measurements (for profiling them alone)")
+    ap.add_argument("--no-eval", action="store_true", help="skip the shadow-eval (LM head + eval statistics) line")
+    ap.add_argument("--eval-only", action="store_true",
+                    help="only the shadow-eval measurement (for profiling it alone)")
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (scale for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -151,6 +161,9 @@ def main():
         F.call("glt_adamw_graft_step", sl, 1, gptr, mptr, vptr, pkptr, 7, i, LR, B1, B2, AEPS, WD, CLIP, p(clip_ws),
                clip_ws_bytes, sp)
 
+    if args.eval_only:
+        print(json.dumps({"shadow_eval": bench_shadow_eval(torch, F, sp, p)}), flush=True)
+        return
     if args.layer_only:
         out = {"attention": bench_attention(torch, F, sp, p),
                "decoder_layer": bench_layer(torch, F, lib, dev, sp, p, fill, base, sl)}
@@ -242,7 +255,7 @@ def main():
     hbm["torch_copy"] = bench_copy(torch)
     del flush_buf, flush_out
     attention = bench_attention(torch, F, sp, p)
-    shadow_eval = bench_shadow_eval(torch, F, sp, p)
+    shadow_eval = None if args.no_eval else bench_shadow_eval(torch, F, sp, p)
     layer = None
     if not args.no_layer:
         layer = bench_layer(torch, F, lib, dev, sp, p, fill, base, sl)

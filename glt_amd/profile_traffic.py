@@ -27,8 +27,11 @@ KERNELS = {
     "rmsnorm_fwd": ("rmsnorm_fwd", None),
     "rmsnorm_bwd": ("rmsnorm_bwd", None),
     "adamw_pack": ("adamw_pack_kernel", None),
-    "rope": ("rope_kernel", None),
+    "rope": ("rope", None),
     "bake": ("bake_kernel", None),
+    "clip_sumsq": ("sumsq_partial_kernel", None),
+    "shuffle_tr": ("shuffle_tr16_kernel<true>", None),
+    "transpose16": ("transpose16_kernel", None),
 }
 
 
