@@ -11,8 +11,9 @@ dy ~N(0,1) in f32 as the reference's backward receives it), drawn on the GPU
 and resident in HBM before timing.
 
 Also measured: shadow_bake materialising 32 layers of baked [15360,4096] /
-[4096,15360] matrices (GB/s against HBM), the HBM-bound kernels, attention
-and the decoder layer, and the reference's graft math in PyTorch on a bounded
+[4096,15360] matrices (GB/s against HBM), the HBM-bound kernels, attention,
+the decoder layer, one shadow-eval batch (LM head and eval statistics at
+16384 x 128256), and the reference's graft math in PyTorch on a bounded
 token sample on the host cores (cpu_baseline).
 
 Prints ONE JSON line. Usage: python bench.py [--steps K] [--warmup W]
@@ -443,8 +444,11 @@ def bench_layer(torch, F, lib, dev, sp, p, fill, base, sl, reps=5):
     query / 8 kv heads of 128, base intermediate 14336, one appended 1024
     slice): glt_layer_fwd, then the graft-only backward of the MLP with
     recompute (glt_mlp_bwd); base weights random, the MLP's shared with the
-    MLP step. Work: MLP fwd + bwd as the step's formulas at 8192 tokens,
-    attention projections 2*M*D*(2*q width + 2*kv width), SDPA 4*B*Hq*T^2*hd/2."""
+    MLP step. The backward recomputes the gate/up pre-activations (the
+    reference's recompute_ffn) and computes the input gradient dX of the
+    MLP as well as the graft gradients. Work: the step's GEMM formulas at
+    8192 tokens plus the recompute (one more gate/up GEMM), attention
+    projections 2*M*D*(2*q width + 2*kv width), SDPA 4*B*Hq*T^2*hd/2."""
     bf = torch.bfloat16
     B, T = ROPE_B, ROPE_T
     Mt, nq, nk = B * T, ROPE_HQ * ROPE_HD, ROPE_HK * ROPE_HD
@@ -468,6 +472,7 @@ def bench_layer(torch, F, lib, dev, sp, p, fill, base, sl, reps=5):
     bd = F.MlpDesc(Mt, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT | F.MLP_RECOMPUTE | F.MLP_DY_F32, 1, sl, None)
     bws = torch.empty(lib.glt_mlp_bwd_workspace_size(ctypes.byref(bd)), dtype=torch.uint8, device=dev)
     grads = torch.zeros(3 * S * D, dtype=torch.float32, device=dev)
+    dx = torch.empty((Mt, D), dtype=torch.float32, device=dev)
     gg = (F.GraftGrads * 1)()
     gg[0] = F.GraftGrads(grads.data_ptr(), grads.data_ptr() + 4 * S * D, grads.data_ptr() + 8 * S * D)
 
@@ -476,7 +481,7 @@ def bench_layer(torch, F, lib, dev, sp, p, fill, base, sl, reps=5):
                p(fws), fws.numel(), sp)
 
     def bwd():
-        F.call("glt_mlp_bwd", ctypes.byref(bd), ctypes.byref(base), p(x_ffn), p(dy), None, None, None, None, gg,
+        F.call("glt_mlp_bwd", ctypes.byref(bd), ctypes.byref(base), p(x_ffn), p(dy), None, None, None, p(dx), gg,
                p(bws), bws.numel(), sp)
 
     fwd()
@@ -492,10 +497,11 @@ def bench_layer(torch, F, lib, dev, sp, p, fill, base, sl, reps=5):
     ev[2].record()
     torch.cuda.synchronize()
     t_f, t_b = ev[0].elapsed_time(ev[1]) / reps, ev[1].elapsed_time(ev[2]) / reps
-    mlp_flop = STEP_FLOP * Mt // M
+    mlp_flop = (STEP_FLOP + GEMM_FLOP["gate_up"]) * Mt // M
     attn_flop = 2 * Mt * D * (2 * nq + 2 * nk) + 4 * B * ROPE_HQ * T * T * ROPE_HD // 2
     ms = t_f + t_b
-    return {"workload": "decoder layer (2 x 4096 tokens, 32/8 heads, grafted MLP) fwd + graft-only bwd with recompute",
+    return {"workload": "decoder layer (2 x 4096 tokens, 32/8 heads, grafted MLP) fwd + the MLP's graft-only bwd "
+                        "(recompute, dX and the graft gradients)",
             "tokens": Mt, "ms_fwd": round(t_f, 4), "ms_bwd": round(t_b, 4), "ms_step": round(ms, 4),
             "tokens_per_s": round(Mt / (ms * 1e-3), 1), "algorithmic_flop": mlp_flop + attn_flop,
             "mfma_frac": round((mlp_flop + attn_flop) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
