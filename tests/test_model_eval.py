@@ -141,3 +141,52 @@ def test_parallel_hash_decomposition_reproduces_the_chain():
         bits = O.f32_to_bf16_bits(x)
         for h in (O.FNV_BASIS, int(rng.integers(0, 2 ** 63)) * 2 + 1):
             assert _parallel_hash(bits, h, chunks) == O.eval_hash_reference(x, h)
+
+
+def _bit_plane_runs(wa, wb):
+    """The low-nibble pass as the GPU runs it (bit planes): bit i of plane j
+    is bit j of run i's nibble, chunk A's 16 runs in the low 16 bits and
+    chunk B's in the high 16 bits of each 32-bit plane. Per logit pair
+    (16-bit patterns a, b): 9 s flips bit 3 by bit 0, XOR with a logit bit
+    is a XOR with that bit spread over its half, 3 s = s + 2 s is a ripple
+    carry over the planes."""
+    M = 0xFFFFFFFF
+
+    def half_mask(w, k):
+        return (0xFFFF if (w >> k) & 1 else 0) | (0xFFFF0000 if (w >> (16 + k)) & 1 else 0)
+
+    def x3(p0, p1, p2, p3):
+        c1, t = p1 & p0, p2 ^ p1
+        c2 = (t & c1) | (~t & p2 & M)
+        return p0, p1 ^ p0, t ^ c1, p3 ^ p2 ^ c2
+
+    p = (0xAAAAAAAA, 0xCCCCCCCC, 0xF0F0F0F0, 0xFF00FF00)   # run i starts at nibble i
+    for a, b in zip(wa, wb):
+        w = int(a) | (int(b) << 16)
+        p0, p1, p2, p3 = p
+        p3 ^= p0 ^ half_mask(w, 3)
+        p = x3(p0 ^ half_mask(w, 0), p1 ^ half_mask(w, 1), p2 ^ half_mask(w, 2), p3)
+        p = x3(*(pj ^ half_mask(w, 8 + j) for j, pj in enumerate(p)))
+    runs = lambda off: [sum(((p[j] >> (off + i)) & 1) << j for j in range(4)) for i in range(16)]
+    return runs(0), runs(16)
+
+
+def test_bit_plane_low_nibble_pass_is_the_chain():
+    """The GPU's bit-plane form of the low-nibble pass gives, for every start
+    nibble and both chunks of a pair, the low nibble that the reference's
+    byte chain reaches (bytes 0, 0, lo, hi per logit)."""
+    rng = np.random.default_rng(5)
+    P = 1099511628211
+
+    def chain(s, ws):
+        for w in ws:
+            for byte in (0, 0, int(w) & 0xFF, int(w) >> 8):
+                s = ((s ^ byte) * P) & 0xFF
+        return s & 15
+
+    for n in (0, 1, 7, 40):
+        wa = rng.integers(0, 1 << 16, n)
+        wb = rng.integers(0, 1 << 16, n)
+        ra, rb = _bit_plane_runs(wa, wb)
+        assert ra == [chain(i, wa) for i in range(16)]
+        assert rb == [chain(i, wb) for i in range(16)]
