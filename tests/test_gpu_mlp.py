@@ -60,6 +60,20 @@ def test_mfma_many_tiles_per_workgroup(dev):
         assert_bf16_budget(r["grads"][0][p], r["rgrads"][0][p], q=2, what=f"dW_{name}")
 
 
+def test_weight_gradients_over_many_tokens(dev):
+    """Few weight-gradient tiles over many tokens (6 tiles, 64 K-steps of
+    4096 tokens each): an appended slice and an in-place slice with an H
+    offset, dX and every gradient against the oracle."""
+    M, D, I = 4096, 256, 512
+    pl = [(I, 128, 0, 256), (64, 128, 128, 128)]
+    N = I + 128
+    r = _run(dev, D, I, N, pl, M, bf16=True)
+    assert_bf16_budget(*r["dx"], q=4, what="dx")
+    for j in range(2):
+        for p, name in enumerate(("gate", "up", "down")):
+            assert_bf16_budget(r["grads"][j][p], r["rgrads"][j][p], q=2, what=f"slice {j} dW_{name}")
+
+
 def test_mfma_many_tiles_explicit_off(dev):
     """Graft columns without a segment (explicit off) are zero-K tiles
     interleaved with full ones in each workgroup's tile sequence."""
