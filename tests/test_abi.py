@@ -55,3 +55,28 @@ def test_host_validation_errors_without_gpu():
     assert lib.glt_rmsnorm_fwd(None, None, None, None, -1, 8, 1e-5, None) == 2
     assert lib.glt_graft_gemm(9, 1, 1, 1, None, 0, None, None, None, 0, 1.0, 0.0, None) == 1
     assert lib.glt_adamw_step(1, 1, 1, 1, None, 10, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1.0, None, 0, None) == 5
+
+
+def test_eval_and_graft_adamw_validation_without_gpu():
+    """glt_eval_stats and the graft AdamW step refuse bad requests, and pass
+    an empty batch through, before any GPU call."""
+    from glt_amd import _ffi as F
+    lib = F.load()
+    res = F.EvalResult()
+    h = 0x0123456789ABCDEF
+    assert lib.glt_eval_stats(1, 8, 1, 1, 2, 8, 5, h, ctypes.byref(res), None, 0, None) == 1   # hash mode
+    assert lib.glt_eval_stats(1, 4, 1, 1, 2, 8, 0, h, ctypes.byref(res), None, 0, None) == 2   # row stride < V
+    assert lib.glt_eval_stats(1, 8, 1, 1, 2, 8, 0, h, ctypes.byref(res), None, 0, None) == 5   # no workspace
+    # no rows: the running hash passes through unchanged (the reference's
+    # chain over an empty batch), nothing counted
+    assert lib.glt_eval_stats(None, 8, None, 0, 2, 8, 0, h, ctypes.byref(res), None, 0, None) == 0
+    assert res.logits_hash == h and res.count == 0 and res.total_nll == 0.0
+    # graft AdamW: 9 slices are more than one call's clip takes (either form);
+    # the clip without its workspace
+    sl = (F.GraftSlice * 9)()
+    arr = F.ptr_array([16] * 9)
+    args = (sl, 9, arr, arr, arr, None, 7, 0, 1e-4, 0.9, 0.999, 1e-8, 0.01)
+    assert lib.glt_adamw_graft_step(*args, 0.0, None, 0, None) == 9
+    assert lib.glt_adamw_graft_step_noalloc(*args, 0.0, None) == 9
+    assert lib.glt_adamw_graft_step(sl, 1, arr, arr, arr, None, 7, 0, 1e-4, 0.9, 0.999, 1e-8, 0.01, 1.0, None, 0,
+                                    None) == 5
