@@ -26,7 +26,7 @@ namespace glt {
 constexpr int kTile = 64;
 // Layers per launch and slices per bake: the launch argument block carries a
 // graft pointer per (layer, slice), 1 KB at 16 x 8. Eight slices cover every
-// stack glt_mlp_fwd / glt_mlp_bwd take (at most 7).
+// stack glt_mlp_fwd / glt_mlp_bwd take (at most 8).
 constexpr int kMaxLayers = 16;
 constexpr int kMaxBakeSlices = 8;
 

@@ -16,7 +16,7 @@
 
 namespace glt {
 
-constexpr int kMaxSeg = 16;
+constexpr int kMaxSeg = 18;  // dX of 8 slices: base gate and up + 2 per slice
 constexpr int kMaxProb = 8;
 
 enum EpiMode : int {

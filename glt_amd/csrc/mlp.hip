@@ -47,7 +47,7 @@ static glt_status check_desc(const glt_mlp_desc* d, const glt_base_weights* w, c
   GLT_CHECK(d->dtype == GLT_DTYPE_BF16 || d->dtype == GLT_DTYPE_F32, GLT_ERR_DTYPE, "%s: dtype %d", who, d->dtype);
   GLT_CHECK(d->M >= 0 && d->D > 0 && d->I >= 0 && d->N >= d->I && d->N > 0, GLT_ERR_SHAPE,
             "%s: bad dims M=%d D=%d I=%d N=%d", who, d->M, d->D, d->I, d->N);
-  GLT_CHECK(d->n_slices >= 0 && d->n_slices <= 7, GLT_ERR_UNSUPPORTED, "%s: %d slices (max 7)", who, d->n_slices);
+  GLT_CHECK(d->n_slices >= 0 && d->n_slices <= 8, GLT_ERR_UNSUPPORTED, "%s: %d slices (max 8)", who, d->n_slices);
   GLT_CHECK(d->n_slices == 0 || d->slices, GLT_ERR_INVALID_ARG, "%s: null slices", who);
   GLT_CHECK(d->I == 0 || (w->gate && w->up && w->down), GLT_ERR_INVALID_ARG, "%s: null base weight", who);
   GLT_CHECK(d->I == 0 || !mlp_uses_mfma(d) || w->prepared, GLT_ERR_INVALID_ARG,

@@ -135,7 +135,7 @@ typedef struct {
   int32_t M, D, I, N;
   int32_t dtype;   /* GLT_DTYPE_BF16 or GLT_DTYPE_F32 */
   int32_t flags;
-  int32_t n_slices;
+  int32_t n_slices;               /* at most 8 (as glt_shadow_bake and the AdamW graft step) */
   const glt_graft_slice* slices;
   glt_model_state* state; /* nullable; checked for the baked guard in backward */
 } glt_mlp_desc;

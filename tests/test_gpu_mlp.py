@@ -98,6 +98,45 @@ def test_mfma_inplace_and_stacked_bf16(dev):
             assert_bf16_budget(r["grads"][j][p], r["rgrads"][j][p], q=2, what=f"slice{j} proj{p}")
 
 
+def test_eight_slices_the_most_one_call_takes(dev):
+    """Eight slices (the limit of glt_mlp_fwd/bwd, glt_shadow_bake and the
+    graft AdamW step): six in place over different neuron and hidden ranges,
+    two appended; 18 K-segments in the dX GEMM. The forward against the
+    oracle; the backward against the oracle's backward fed by the kernel's
+    own saved activations (so that a pre-activation one bf16 ulp away from
+    the oracle's at a rounding boundary, which moves inter and through it
+    the small dW_down entries, is not counted against the backward)."""
+    import torch
+    from glt_amd import ops, synth
+    M, D, I = 256, 256, 512
+    pl = [(0, 64, 0, 128), (64, 64, 128, 128), (128, 64, 64, 192), (192, 64, 0, 256),
+          (320, 64, 192, 64), (448, 64, 0, 64), (512, 64, 0, 256), (576, 128, 64, 128)]
+    N = 704
+    bf = torch.bfloat16
+    wg, wu, wd, sl = make_layer(D, I, N, pl, True)
+    x = draw((M, D), 100, synth.TID_X, 0, 1, True)
+    dy = draw((M, D), 200, synth.TID_DY, 0, 1, True)
+    base = ops.BaseMLP(to_dev(wg, bf), to_dev(wu, bf), to_dev(wd, bf))
+    gs = [ops.GraftSlice(s["i0"], s["s"], s["h0"], s["h"],
+                         *(to_dev(s[p], torch.float32) for p in ("gate", "up", "down"))).pack() for s in sl]
+    xd, dyd = to_dev(x, bf), to_dev(dy, bf)
+    y, gp, up, inter = ops.mlp_forward(base, gs, xd, N)
+    dx, grads = ops.mlp_backward(base, gs, xd, dyd, N, gp, up, inter)
+    torch.cuda.synchronize()
+    rg, ru, ri, ry = O.mlp_fwd(x, wg, wu, wd, N, sl, bf16=True)
+    for name, a, ref, q in (("g", gp, rg, 2), ("u", up, ru, 2), ("y", y, ry, 4)):
+        assert_bf16_budget(to_np(a), ref, q=q, what=name)
+    g_k, u_k, i_k = to_np(gp), to_np(up), to_np(inter)
+    # inter from the kernel's own g and u: one rounding
+    assert_bf16_budget(i_k, O.silu_mul(g_k, u_k), q=1, what="inter from the kernel's g, u")
+    assert rel_l2(i_k, ri) <= 1e-2
+    rdx, rgrads = O.mlp_bwd(x, wg, wu, wd, N, sl, g_k, u_k, i_k, dy, bf16=True)
+    assert_bf16_budget(to_np(dx), rdx, q=4, what="dx")
+    for j in range(len(pl)):
+        for p in range(3):
+            assert_bf16_budget(to_np(grads[j][p]), rgrads[j][p], q=2, what=f"slice{j} proj{p}")
+
+
 def test_f32_config1(dev):
     """Config 1: hidden 512, base 1408, 256 appended neurons, 4x128 tokens, fp32."""
     M, D, I, S = 512, 512, 1408, 256
