@@ -222,7 +222,8 @@ def main():
     # HBM-bound kernels against the HBM roofline. RMSNorm, the clip and the
     # AdamW update: their launches in the step above, each bracketed by HIP
     # events on the launch stream (so in the step's own cache state; the
-    # bracket adds about a microsecond). RoPE at the decoder-layer shape
+    # bracket adds 5-9 us to a launch against rocprofv3's kernel duration,
+    # so these fractions are lower bounds). RoPE at the decoder-layer shape
     # (2 x 4096 tokens, 32 q / 8 kv heads of 128, theta 5e5): one launch at a
     # time, after a read of a 1 GiB buffer that leaves none of its inputs in
     # the caches (the 256 MB last-level cache would otherwise hold the whole
