@@ -137,6 +137,64 @@ def test_eight_slices_the_most_one_call_takes(dev):
             assert_bf16_budget(to_np(grads[j][p]), rgrads[j][p], q=2, what=f"slice{j} proj{p}")
 
 
+def _random_layer(seed):
+    """A random layer the MFMA path takes: a ragged token count, hidden and
+    base widths multiples of 64, 1-4 slices in place or appended with
+    neuron and hidden offsets on 32-element boundaries (so slice ranges
+    straddle the 256-wide tiles and start mid-way through 64-wide K
+    blocks), and 0-7 groups of 8 trailing columns that no slice covers."""
+    rng = np.random.default_rng(seed)
+    M = int(rng.integers(1, 700))
+    D = 64 * int(rng.integers(1, 9))
+    I = 64 * int(rng.integers(1, 13))
+    pl, n = [], I
+    for _ in range(int(rng.integers(1, 5))):
+        s = 64 * int(rng.integers(1, 4))
+        h = 64 * int(rng.integers(1, D // 64 + 1))
+        h0 = 32 * int(rng.integers(0, (D - h) // 32 + 1))
+        if rng.random() < 0.6 and s <= I:
+            i0 = 32 * int(rng.integers(0, (I - s) // 32 + 1))
+        else:
+            i0, n = n, n + s
+        pl.append((i0, s, h0, h))
+    return M, D, I, n + 8 * int(rng.integers(0, 8)), pl
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_mfma_random_layers(dev, seed):
+    """Random layer shapes (`_random_layer`) through the forward and the
+    graft-only backward: the forward against the oracle, inter against
+    silu(g)*u of the kernel's own pre-activations, and the backward against
+    the oracle's backward fed by the kernel's saved activations (as in the
+    eight-slice test)."""
+    import torch
+    from glt_amd import ops, synth
+    M, D, I, N, pl = _random_layer(seed)
+    case = f"seed {seed}: M={M} D={D} I={I} N={N} slices={pl}"
+    bf = torch.bfloat16
+    wg, wu, wd, sl = make_layer(D, I, N, pl, True)
+    x = draw((M, D), 100 + seed, synth.TID_X, 0, 1, True)
+    dy = draw((M, D), 200 + seed, synth.TID_DY, 0, 1, True)
+    base = ops.BaseMLP(to_dev(wg, bf), to_dev(wu, bf), to_dev(wd, bf))
+    gs = [ops.GraftSlice(s["i0"], s["s"], s["h0"], s["h"],
+                         *(to_dev(s[p], torch.float32) for p in ("gate", "up", "down"))).pack() for s in sl]
+    xd, dyd = to_dev(x, bf), to_dev(dy, bf)
+    y, gp, up, inter = ops.mlp_forward(base, gs, xd, N)
+    dx, grads = ops.mlp_backward(base, gs, xd, dyd, N, gp, up, inter)
+    torch.cuda.synchronize()
+    rg, ru, ri, ry = O.mlp_fwd(x, wg, wu, wd, N, sl, bf16=True)
+    for name, a, ref, q in (("g", gp, rg, 2), ("u", up, ru, 2), ("y", y, ry, 4)):
+        assert_bf16_budget(to_np(a), ref, q=q, what=f"{case}: {name}")
+    g_k, u_k, i_k = to_np(gp), to_np(up), to_np(inter)
+    assert_bf16_budget(i_k, O.silu_mul(g_k, u_k), q=1, what=f"{case}: inter from the kernel's g, u")
+    assert rel_l2(i_k, ri) <= 1e-2, case
+    rdx, rgrads = O.mlp_bwd(x, wg, wu, wd, N, sl, g_k, u_k, i_k, dy, bf16=True)
+    assert_bf16_budget(to_np(dx), rdx, q=4, what=f"{case}: dx")
+    for j in range(len(pl)):
+        for p in range(3):
+            assert_bf16_budget(to_np(grads[j][p]), rgrads[j][p], q=2, what=f"{case}: slice{j} proj{p}")
+
+
 def test_f32_config1(dev):
     """Config 1: hidden 512, base 1408, 256 appended neurons, 4x128 tokens, fp32."""
     M, D, I, S = 512, 512, 1408, 256
