@@ -236,7 +236,7 @@ def main():
                       "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "timing": "in the step"}
     flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
     flush_buf.fill_(1.0)
-    flush_out = torch.empty(1, dtype=torch.float32, device=dev)
+    flush_out = torch.empty((), dtype=torch.float32, device=dev)
 
     def cold_ms(fn, reps=20):
         fn()
