@@ -219,38 +219,39 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                 "traffic_source": traffic_source, "flop_per_launch": dom_flop}
 
-    # HBM-bound kernels against the HBM roofline. RMSNorm, the clip and the
-    # AdamW update: their launches in the step above, each bracketed by HIP
-    # events on the launch stream (so in the step's own cache state; the
-    # bracket adds 5-9 us to a launch against rocprofv3's kernel duration,
-    # so these fractions are lower bounds). RoPE at the decoder-layer shape
-    # (2 x 4096 tokens, 32 q / 8 kv heads of 128, theta 5e5): one launch at a
-    # time, after a read of a 1 GiB buffer that leaves none of its inputs in
-    # the caches (the 256 MB last-level cache would otherwise hold the whole
+    # HBM-bound kernels against the HBM roofline. RMSNorm, the clip, the
+    # layout passes and the AdamW update: their launches in the step above
+    # (so in the step's own cache state), each timed by HIP events bound to
+    # its dispatch (hipExtLaunchKernelGGL: the kernel's execution time, as a
+    # kernel trace reports it). RoPE at the decoder-layer shape (2 x 4096
+    # tokens, 32 q / 8 kv heads of 128, theta 5e5): one launch at a time,
+    # after a read of a 1 GiB buffer that leaves none of its inputs in the
+    # caches (the 256 MB last-level cache would otherwise hold the whole
     # input across repeated launches).
     hbm = {}
     for k, nbytes in HBM_BYTES.items():
         if k in kernels:
             t = kernels[k]["avg_ms"]
             hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
-                      "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "timing": "in the step"}
+                      "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                      "timing": "kernel duration in the step (events bound to the dispatch)"}
     flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
     flush_buf.fill_(1.0)
     flush_out = torch.empty((), dtype=torch.float32, device=dev)
 
-    def cold_ms(fn, reps=20):
+    def cold_ms(fn, label, reps=20):
+        # each launch after a 1 GiB read; its duration from the launch timing
+        # (events bound to the kernel dispatch)
         fn()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        tot = 0.0
+        F.call("glt_profile_enable", 1)
         for _ in range(reps):
             torch.sum(flush_buf, 0, out=flush_out)
-            e0.record(stream)
             fn()
-            e1.record(stream)
-            e1.synchronize()
-            tot += e0.elapsed_time(e1)
-        return tot / reps
+        torch.cuda.synchronize()
+        tot, cnt = F.profile_collect().get(label, (0.0, 1))
+        F.call("glt_profile_enable", 0)
+        return tot / cnt
 
     hbm["rope"] = bench_rope(torch, F, sp, p, cold_ms)
     hbm["masked_ce"] = bench_masked_ce(torch, F, sp, p)
@@ -313,11 +314,11 @@ def bench_rope(torch, F, sp, p, cold_ms):
     def run():
         F.call("glt_rope_fwd", p(q), ROPE_HQ, p(k), ROPE_HK, ROPE_B, ROPE_T, ROPE_HD, ROPE_THETA, 0, sp)
 
-    t = cold_ms(run)
+    t = cold_ms(run, "rope")
     nbytes = 2 * 2 * ROPE_B * ROPE_T * (ROPE_HQ + ROPE_HK) * ROPE_HD
     return {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-            "timing": "one launch after a 1 GiB read, events around it"}
+            "timing": "kernel duration (events bound to the dispatch), each launch after a 1 GiB read"}
 
 
 def bench_shadow_eval(torch, F, sp, p, reps=3):

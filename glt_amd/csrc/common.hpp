@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
 
@@ -31,18 +32,22 @@ glt_status hip_fail(hipError_t e, const char* what);
 // Checks the launch that was just issued.
 #define GLT_LAUNCH_CHECK(name) GLT_TRY_HIP(hipGetLastError())
 
-// Launch timing: while glt_profile_enable(1) is in effect, prof_begin /
-// prof_end bracket a launch with HIP events recorded on its stream (no
-// synchronisation; glt_profile_collect resolves them later).
-int prof_begin(const char* label, hipStream_t st);  // returns a record id or -1
-void prof_end(int id, hipStream_t st);
+// Launch timing: while glt_profile_enable(1) is in effect, prof_slot hands
+// out a pair of pooled HIP events for a launch (or returns -1), and the
+// launch goes through hipExtLaunchKernelGGL, which binds both events to the
+// kernel dispatch itself: their elapsed time is the kernel's execution time
+// (as a kernel trace reports it), without the gaps that event records
+// placed on the stream around a launch add.
+int prof_slot(const char* label, hipEvent_t* start, hipEvent_t* stop);  // record id or -1
 
 // Launch with optional timing under `label`.
-#define GLT_LAUNCH(label, kernel, grid, block, shmem, st, ...)            \
-  do {                                                                    \
-    const int _pid = ::glt::prof_begin(label, st);                        \
-    hipLaunchKernelGGL(kernel, grid, block, shmem, st, __VA_ARGS__);      \
-    ::glt::prof_end(_pid, st);                                            \
+#define GLT_LAUNCH(label, kernel, grid, block, shmem, st, ...)                                   \
+  do {                                                                                           \
+    hipEvent_t _e0 = nullptr, _e1 = nullptr;                                                     \
+    if (::glt::prof_slot(label, &_e0, &_e1) >= 0)                                                \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, _e0, _e1, 0, __VA_ARGS__);           \
+    else                                                                                         \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, st, __VA_ARGS__);                           \
   } while (0)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

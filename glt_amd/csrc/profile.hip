@@ -1,7 +1,8 @@
 // Per-label launch timing with HIP events (the reference's
 // --profile-graft-gemms, src/gemm_impl.inc:153-199 and :408-444, keeps one
 // event pair per GEMM and synchronises after each; here events are taken
-// from a pool created up front and resolved in one pass at collect time, so
+// from a pool created up front, bound to the kernel dispatch by
+// hipExtLaunchKernelGGL, and resolved in one pass at collect time, so
 // profiled runs keep the stream busy).
 #include <cstring>
 #include <mutex>
@@ -25,21 +26,16 @@ int g_next = 0;
 constexpr int kPool = 16384;
 }  // namespace
 
-int prof_begin(const char* label, hipStream_t st) {
+int prof_slot(const char* label, hipEvent_t* start, hipEvent_t* stop) {
   if (!g_on) return -1;
   std::lock_guard<std::mutex> lk(g_mu);
   if (g_next + 2 > (int)g_pool.size()) return -1;
   const int a = g_next, b = g_next + 1;
   g_next += 2;
-  if (hipEventRecord(g_pool[a], st) != hipSuccess) return -1;
+  *start = g_pool[a];
+  *stop = g_pool[b];
   g_recs.push_back(Rec{label, a, b});
   return (int)g_recs.size() - 1;
-}
-
-void prof_end(int id, hipStream_t st) {
-  if (id < 0) return;
-  std::lock_guard<std::mutex> lk(g_mu);
-  (void)hipEventRecord(g_pool[g_recs[id].b], st);
 }
 
 }  // namespace glt
