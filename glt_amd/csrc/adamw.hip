@@ -15,47 +15,46 @@ constexpr int kClipMaxSegs = 24;  // 3 projections x up to 8 slices
 
 // The gradient vectors one clip norm covers: partial sums of g^2 (f32, like
 // the reference reduce_l2_kernel, src/kernels_elementwise_impl.inc:141-165),
-// one partial per workgroup over every listed vector.
+// one partial per workgroup. Workgroup b covers elements
+// [(b - blk0[j]) * chunk, ...+chunk) of segment j, blk0[j] <= b < blk0[j+1].
 struct ClipSegs {
   const float* g[kClipMaxSegs];
   int64_t n[kClipMaxSegs];
+  int blk0[kClipMaxSegs + 1];
+  int64_t chunk;  // elements per workgroup, a multiple of 1024
   int nseg;
 };
 
 __global__ void __launch_bounds__(256) sumsq_partial_kernel(const ClipSegs segs, float* __restrict__ partial) {
   __shared__ float wsum[4];
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < segs.nseg && b >= segs.blk0[j + 1]) ++j;
+  const float* g = segs.g[j];
+  const int64_t lo = (int64_t)(b - segs.blk0[j]) * segs.chunk;
+  const int64_t hi = min(lo + segs.chunk, segs.n[j]);
   float s = 0.f;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (int j = 0; j < segs.nseg; ++j) {
-    const float* g = segs.g[j];
-    const int64_t n = segs.n[j];
-    int64_t done = 0;
-    if ((reinterpret_cast<uintptr_t>(g) & 15) == 0) {
-      // 16-byte loads over the whole multiple-of-4 prefix, four in flight
-      const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
-      const int64_t n4 = n / 4;
-      int64_t i = first;
-      for (; i + 3 * stride < n4; i += 4 * stride) {
-        f32x4 v[4];
+  if ((reinterpret_cast<uintptr_t>(g) & 15) == 0) {
+    // 16-byte loads, eight in flight per thread before any is summed
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
+    const int64_t lo4 = lo / 4, hi4 = hi / 4;  // chunk % 4 == 0: lo4 * 4 == lo
+    constexpr int U = 8;
+    for (int64_t i0 = lo4 + threadIdx.x; i0 < hi4; i0 += 256 * U) {
+      f32x4 v[U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = g4[i + u * stride];
+      for (int u = 0; u < U; ++u) v[u] = i0 + 256 * u < hi4 ? g4[i0 + 256 * u] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) s += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
-      }
-      for (; i < n4; i += stride) {
-        const f32x4 v = g4[i];
-        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-      }
-      done = n4 * 4;
+      for (int u = 0; u < U; ++u) s += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
     }
-    for (int64_t i = done + first; i < n; i += stride) s += g[i] * g[i];
+    for (int64_t i = hi4 * 4 + threadIdx.x; i < hi; i += 256) s += g[i] * g[i];
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) s += g[i] * g[i];
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
   __syncthreads();
-  if (threadIdx.x == 0) partial[blockIdx.x] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  if (threadIdx.x == 0) partial[b] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
 }
 
 // scale = clip/norm if norm > clip else 1, norm = sqrt(sum + 1e-8)
@@ -75,10 +74,28 @@ __device__ float block_clip_scale(const float* __restrict__ partial, int np, flo
 }
 
 // The partials of a clip over segs: ws[0, np). Returns np through *np_out.
-glt_status launch_clip(const ClipSegs& segs, float* ws, size_t ws_floats, int* np_out, hipStream_t st) {
+glt_status launch_clip(const ClipSegs& segs_in, float* ws, size_t ws_floats, int* np_out, hipStream_t st) {
+  ClipSegs segs = segs_in;
   int64_t total = 0;
   for (int j = 0; j < segs.nseg; ++j) total += segs.n[j];
-  const int np = (int)std::max<int64_t>(1, std::min<int64_t>(kClipBlocks, cdiv(total, 1024)));
+  // the smallest chunk (a multiple of 1024) whose workgroups over all
+  // segments number at most kClipBlocks
+  int64_t chunk = std::max<int64_t>(1024, cdiv(cdiv(total, kClipBlocks), 1024) * 1024);
+  auto blocks = [&](int64_t c) {
+    int64_t nb = 0;
+    for (int j = 0; j < segs.nseg; ++j) nb += cdiv(segs.n[j], c);
+    return nb;
+  };
+  while (blocks(chunk) > kClipBlocks) chunk += 1024;
+  segs.chunk = chunk;
+  int np = 0;
+  for (int j = 0; j < segs.nseg; ++j) {
+    segs.blk0[j] = np;
+    np += (int)cdiv(segs.n[j], chunk);
+  }
+  // nothing to sum (every segment empty): one workgroup writes a zero partial
+  if (np == 0) np = 1;
+  segs.blk0[segs.nseg] = np;
   GLT_CHECK((size_t)np <= ws_floats, GLT_ERR_WORKSPACE, "adamw clip: %d partial sums, room for %zu", np, ws_floats);
   GLT_LAUNCH("clip_sumsq", sumsq_partial_kernel, dim3(np), dim3(256), 0, st, segs, ws);
   GLT_LAUNCH_CHECK("sumsq_partial");

@@ -58,10 +58,16 @@ __global__ void __launch_bounds__(64 * kFwdWaves) rmsnorm_fwd_vec(const uint16_t
   const int64_t row = blockIdx.x;
   const int nch = D >> 3;
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * D);
-  u32x4 xv[NC];
+  const u32x4* wr = reinterpret_cast<const u32x4*>(w);
+  // the row and its weight chunks are loaded together, so no load waits
+  // behind the row reduction
+  u32x4 xv[NC], wv[NC];
 #pragma unroll
   for (int i = 0; i < NC; ++i)
-    if (c0 + 64 * i < nch) xv[i] = __builtin_nontemporal_load(xr + c0 + 64 * i);
+    if (c0 + 64 * i < nch) {
+      xv[i] = __builtin_nontemporal_load(xr + c0 + 64 * i);
+      wv[i] = wr[c0 + 64 * i];
+    }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i)
@@ -74,7 +80,6 @@ __global__ void __launch_bounds__(64 * kFwdWaves) rmsnorm_fwd_vec(const uint16_t
   const float v = row_sum<kFwdWaves>(ss, part) / (float)D;
   const float r = rsqrtf(v + eps);
   if (threadIdx.x == 0) var[row] = v;
-  const u32x4* wr = reinterpret_cast<const u32x4*>(w);
   u32x4* yr = reinterpret_cast<u32x4*>(y + row * D);
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -82,7 +87,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) rmsnorm_fwd_vec(const uint16_t
     if (c < nch) {
       float f[8], g[8];
       unpack8(xv[i], f);
-      unpack8(wr[c], g);
+      unpack8(wv[i], g);
       u32x4 o;
       o.x = pack_bf16x2(f[0] * r * g[0], f[1] * r * g[1]);
       o.y = pack_bf16x2(f[2] * r * g[2], f[3] * r * g[3]);
@@ -134,13 +139,14 @@ __global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* _
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * D);
   const u32x4* wr = reinterpret_cast<const u32x4*>(w);
   const f32x4* dyr = reinterpret_cast<const f32x4*>(dy + row * D);
-  u32x4 xv[NC];
+  u32x4 xv[NC], wv[NC];
   f32x4 d0[NC], d1[NC];
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = c0 + 64 * i;
     if (c < nch) {
       xv[i] = __builtin_nontemporal_load(xr + c);
+      wv[i] = wr[c];
       d0[i] = dyr[2 * c];
       d1[i] = dyr[2 * c + 1];
     }
@@ -152,7 +158,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* _
     if (c < nch) {
       float f[8], g[8];
       unpack8(xv[i], f);
-      unpack8(wr[c], g);
+      unpack8(wv[i], g);
       acc += d0[i].x * f[0] * g[0] + d0[i].y * f[1] * g[1] + d0[i].z * f[2] * g[2] + d0[i].w * f[3] * g[3];
       acc += d1[i].x * f[4] * g[4] + d1[i].y * f[5] * g[5] + d1[i].z * f[6] * g[6] + d1[i].w * f[7] * g[7];
     }
@@ -165,7 +171,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* _
     if (c < nch) {
       float f[8], g[8];
       unpack8(xv[i], f);
-      unpack8(wr[c], g);
+      unpack8(wv[i], g);
       f32x4 o0, o1;
       o0.x = d0[i].x * r * g[0] - f[0] * mean * r3;
       o0.y = d0[i].y * r * g[1] - f[1] * mean * r3;
