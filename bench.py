@@ -156,9 +156,10 @@ def main():
     def step(i):
         F.call("glt_rmsnorm_fwd", p(x_raw), p(gamma), p(x), p(var), M, D, EPS, sp)
         F.call("glt_mlp_fwd", ctypes.byref(desc), ctypes.byref(base), p(x), p(y), p(g), p(u), p(inter), sp)
-        F.call("glt_mlp_bwd", ctypes.byref(desc), ctypes.byref(base), p(x), p(dy), p(g), p(u), p(inter), p(dx), gg,
-               p(ws), ws_bytes, sp)
-        F.call("glt_rmsnorm_bwd", p(dx), p(x_raw), p(gamma), p(var), p(dx_raw), M, D, EPS, sp)
+        # graft-only backward and the RMSNorm's backward (the latter on the
+        # CUs the weight-gradient GEMM leaves idle)
+        F.call("glt_mlp_rmsnorm_bwd", ctypes.byref(desc), ctypes.byref(base), p(x), p(dy), p(g), p(u), p(inter),
+               p(dx), gg, p(ws), ws_bytes, p(x_raw), p(gamma), p(var), EPS, p(dx_raw), sp)
         F.call("glt_adamw_graft_step", sl, 1, gptr, mptr, vptr, pkptr, 7, i, LR, B1, B2, AEPS, WD, CLIP, p(clip_ws),
                clip_ws_bytes, sp)
 
@@ -228,8 +229,26 @@ def main():
     # after a read of a 1 GiB buffer that leaves none of its inputs in the
     # caches (the 256 MB last-level cache would otherwise hold the whole
     # input across repeated launches).
+    # The step's RMSNorm backward runs beside the weight-gradient GEMM on
+    # the CUs that launch leaves idle (label rmsnorm_bwd_beside), so its
+    # duration there says nothing about bandwidth: glt_rmsnorm_bwd is timed
+    # on its own over the step's buffers.
+    F.call("glt_profile_enable", 1)
+    for _ in range(args.steps):
+        F.call("glt_rmsnorm_bwd", p(dx), p(x_raw), p(gamma), p(var), p(dx_raw), M, D, EPS, sp)
+    torch.cuda.synchronize()
+    tot, cnt = F.profile_collect().get("rmsnorm_bwd", (0.0, 1))
+    F.call("glt_profile_enable", 0)
+    rms_bwd_alone = tot / cnt
     hbm = {}
     for k, nbytes in HBM_BYTES.items():
+        if k == "rmsnorm_bwd":
+            t = rms_bwd_alone
+            hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),
+                      "frac_hbm": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                      "timing": "kernel duration, launched alone on the step's buffers (in the step it runs "
+                                "beside the weight-gradient GEMM)"}
+            continue
         if k in kernels:
             t = kernels[k]["avg_ms"]
             hbm[k] = {"bytes": nbytes, "ms": round(t, 5), "GB_per_s": round(nbytes / (t * 1e-3) / 1e9, 1),

@@ -112,6 +112,8 @@ SIGNATURES = {
     "glt_mlp_bwd_workspace_size": (_sz, [ctypes.POINTER(MlpDesc)]),
     "glt_mlp_bwd": (_i32, [ctypes.POINTER(MlpDesc), ctypes.POINTER(BaseWeights), _vp, _vp, _vp, _vp, _vp, _vp,
                            ctypes.POINTER(GraftGrads), _vp, _sz, _vp]),
+    "glt_mlp_rmsnorm_bwd": (_i32, [ctypes.POINTER(MlpDesc), ctypes.POINTER(BaseWeights), _vp, _vp, _vp, _vp, _vp,
+                                   _vp, ctypes.POINTER(GraftGrads), _vp, _sz, _vp, _vp, _vp, _f32, _vp, _vp]),
     "glt_silu_mul": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "glt_gate_up_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "glt_rmsnorm_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),

@@ -805,7 +805,7 @@ bool gemm_mfma_eligible(const GemmPlan& plan) {
 // CUs of the current device (the persistent grid size), cached per device.
 // The caches are atomics: host threads making their first calls at the same
 // time may both query the device (the same value), never race on the slot.
-static glt_status device_cus(int& cus) {
+glt_status device_cus(int& cus) {
   static std::atomic<int> cached[64];
   int dev = 0;
   GLT_TRY_HIP(hipGetDevice(&dev));
@@ -851,6 +851,14 @@ static glt_status launch_generic(const GArgs& a, hipStream_t st, const char* lab
   GLT_LAUNCH(label, (gemm_generic_kernel<LA, LB, TO, MODE, DUAL>), dim3(a.total_tiles), dim3(256), 0, st, a);
   GLT_LAUNCH_CHECK("gemm_generic");
   return GLT_OK;
+}
+
+int gemm_mfma_tiles(const GemmPlan& plan) {
+  const int bn = plan.dual ? 128 : 256;
+  int tiles = 0;
+  for (int p = 0; p < plan.args.nprob; ++p)
+    tiles += (int)(cdiv(plan.args.p[p].M, kBM) * cdiv(plan.args.p[p].N, bn));
+  return tiles;
 }
 
 glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma) {

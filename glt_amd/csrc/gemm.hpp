@@ -86,5 +86,10 @@ struct GemmPlan {
 // form: such a plan must be MFMA-eligible.
 glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma = true);
 bool gemm_mfma_eligible(const GemmPlan& plan);
+// Workgroups of the MFMA kernel's launch for this plan (one per 256 x 256
+// tile, dual: 256 x 128, at most one per CU).
+int gemm_mfma_tiles(const GemmPlan& plan);
+// CUs of the current device (cached per device).
+glt_status device_cus(int& cus);
 
 }  // namespace glt

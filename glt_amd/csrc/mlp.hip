@@ -2,9 +2,12 @@
 // base preparation. Host code that turns a glt_mlp_desc into segment-list
 // GEMM launches (see gemm.hpp).
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "gemm.hpp"
 #include "layout.hpp"
+#include "norm_rope.hpp"
 
 namespace glt {
 
@@ -248,9 +251,64 @@ size_t glt_mlp_bwd_workspace_size(const glt_mlp_desc* d) {
   return bwd_layout(d).total;
 }
 
-glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, const void* dy,
-                       const void* gate_pre, const void* up_pre, const void* inter, float* dx,
-                       const glt_graft_grads* grads, void* ws, size_t ws_bytes, void* stream) {
+namespace glt {
+// The RMSNorm backward that glt_mlp_rmsnorm_bwd runs after the MLP backward.
+struct NormBwd {
+  const uint16_t* x;
+  const uint16_t* w;
+  const float* var;
+  float eps;
+  float* dx;
+};
+
+// Helper stream of the current device (created once, default priority) on
+// which the RMSNorm backward runs beside the weight-gradient GEMM.
+static glt_status helper_stream(hipStream_t& out) {
+  static std::atomic<hipStream_t> streams[64];
+  static std::mutex mu;
+  int dev = 0;
+  GLT_TRY_HIP(hipGetDevice(&dev));
+  GLT_CHECK(dev >= 0 && dev < 64, GLT_ERR_HIP, "helper stream: device index %d out of range", dev);
+  hipStream_t h = streams[dev].load(std::memory_order_acquire);
+  if (!h) {
+    std::lock_guard<std::mutex> lk(mu);
+    h = streams[dev].load(std::memory_order_acquire);
+    if (!h) {
+      GLT_TRY_HIP(hipStreamCreateWithFlags(&h, hipStreamNonBlocking));
+      streams[dev].store(h, std::memory_order_release);
+    }
+  }
+  out = h;
+  return GLT_OK;
+}
+
+// Starts the RMSNorm backward of dx on the helper stream once everything
+// enqueued on st so far is done, on `grid` persistent workgroups; *done is
+// recorded on the helper stream after it (the caller waits for it on st and
+// destroys it).
+static glt_status fork_norm_bwd(const NormBwd& nb, const float* dx, int M, int D, int grid, hipStream_t st,
+                                hipEvent_t* done) {
+  hipStream_t hs = nullptr;
+  glt_status s = helper_stream(hs);
+  if (s != GLT_OK) return s;
+  hipEvent_t ready = nullptr;
+  GLT_TRY_HIP(hipEventCreateWithFlags(&ready, hipEventDisableTiming));
+  GLT_TRY_HIP(hipEventRecord(ready, st));
+  GLT_TRY_HIP(hipStreamWaitEvent(hs, ready, 0));
+  GLT_TRY_HIP(hipEventDestroy(ready));
+  if ((s = rmsnorm_bwd_rows(dx, nb.x, nb.w, nb.var, nb.dx, M, D, nb.eps, grid, hs)) != GLT_OK) return s;
+  GLT_TRY_HIP(hipEventCreateWithFlags(done, hipEventDisableTiming));
+  GLT_TRY_HIP(hipEventRecord(*done, hs));
+  return GLT_OK;
+}
+
+// glt_mlp_bwd; with nb, the RMSNorm backward of dx starts beside the
+// weight-gradient GEMM when that launch leaves CUs idle (*norm_done set),
+// else the caller runs it afterwards.
+static glt_status mlp_bwd_impl(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, const void* dy,
+                               const void* gate_pre, const void* up_pre, const void* inter, float* dx,
+                               const glt_graft_grads* grads, void* ws, size_t ws_bytes, hipStream_t st,
+                               const NormBwd* nb, bool* norm_done) {
   glt_status s = check_desc(d, w, "glt_mlp_bwd");
   if (s != GLT_OK) return s;
   GLT_CHECK(!(d->state && d->state->baked), GLT_ERR_BAKED_NO_BACKWARD,
@@ -264,7 +322,6 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
   GLT_CHECK(ws_bytes >= L.total && (L.total == 0 || ws), GLT_ERR_WORKSPACE,
             "glt_mlp_bwd: workspace %zu bytes < required %zu", ws_bytes, L.total);
   if (d->M == 0) return GLT_OK;
-  hipStream_t st = as_stream(stream);
   char* W = static_cast<char*>(ws);
   const bool f32 = d->dtype == GLT_DTYPE_F32;
   const bool mfma = mlp_uses_mfma(d);
@@ -433,7 +490,24 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
         plan.add_seg(nt_seg(AT, M, 0, M, 0, sl.h, p < 2 ? XS : DYS, M, -sl.h_start));
       }
     }
-    return run_gemm(plan, st);
+    // The weight-gradient launch has few tiles (3 per slice and 256 x 256
+    // block of [S,H]); the CUs it leaves idle take the RMSNorm backward,
+    // which only needs dx (complete: its GEMM ran above on this stream).
+    hipEvent_t norm_ev = nullptr;
+    if (nb && dx && gemm_mfma_eligible(plan) &&
+        rmsnorm_bwd_rows_ok(dx, nb->x, nb->w, nb->dx, d->M, d->D)) {
+      int cus = 0;
+      if ((s = device_cus(cus)) != GLT_OK) return s;
+      const int idle = cus - gemm_mfma_tiles(plan);
+      if (idle >= 16 && (s = fork_norm_bwd(*nb, dx, d->M, d->D, idle, st, &norm_ev)) != GLT_OK) return s;
+    }
+    if ((s = run_gemm(plan, st)) != GLT_OK) return s;
+    if (norm_ev) {
+      GLT_TRY_HIP(hipStreamWaitEvent(st, norm_ev, 0));
+      GLT_TRY_HIP(hipEventDestroy(norm_ev));
+      *norm_done = true;
+    }
+    return GLT_OK;
   }
   // strided (generic) form: A(s, t) = src[t*N + i0 + s], B(h, t) = src2[t*D + h0 + h]
   GemmPlan plan;
@@ -464,6 +538,32 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const v
     }
   }
   return run_gemm(plan, st);
+}
+}  // namespace glt
+
+glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, const void* dy,
+                       const void* gate_pre, const void* up_pre, const void* inter, float* dx,
+                       const glt_graft_grads* grads, void* ws, size_t ws_bytes, void* stream) {
+  bool norm_done = false;
+  return mlp_bwd_impl(d, w, x, dy, gate_pre, up_pre, inter, dx, grads, ws, ws_bytes, as_stream(stream), nullptr,
+                      &norm_done);
+}
+
+glt_status glt_mlp_rmsnorm_bwd(const glt_mlp_desc* d, const glt_base_weights* w, const void* x, const void* dy,
+                               const void* gate_pre, const void* up_pre, const void* inter, float* dx,
+                               const glt_graft_grads* grads, void* ws, size_t ws_bytes, const uint16_t* norm_x,
+                               const uint16_t* norm_w, const float* norm_var, float eps, float* norm_dx,
+                               void* stream) {
+  GLT_CHECK(d, GLT_ERR_INVALID_ARG, "glt_mlp_rmsnorm_bwd: null descriptor");
+  GLT_CHECK(d->M == 0 || (dx && norm_x && norm_w && norm_var && norm_dx), GLT_ERR_INVALID_ARG,
+            "glt_mlp_rmsnorm_bwd: null dx or RMSNorm operand");
+  GLT_CHECK(d->dtype == GLT_DTYPE_BF16, GLT_ERR_DTYPE, "glt_mlp_rmsnorm_bwd: bf16 path only (dtype %d)", d->dtype);
+  const NormBwd nb{norm_x, norm_w, norm_var, eps, norm_dx};
+  bool norm_done = false;
+  hipStream_t st = as_stream(stream);
+  glt_status s = mlp_bwd_impl(d, w, x, dy, gate_pre, up_pre, inter, dx, grads, ws, ws_bytes, st, &nb, &norm_done);
+  if (s != GLT_OK || norm_done || d->M == 0) return s;
+  return glt_rmsnorm_bwd(dx, norm_x, norm_w, norm_var, norm_dx, d->M, d->D, eps, stream);
 }
 
 glt_status glt_graft_gemm(int32_t kind, int32_t M, int32_t S, int32_t H, const uint16_t* a, int64_t lda,

@@ -12,9 +12,11 @@
 // kernel that leaves the last-level cache full of dirty lines (the optimizer
 // step before the next forward) plain loads of x took 50 % longer; dy (just
 // written by the dX GEMM) and the outputs (the next GEMM's input) are plain.
+#include <atomic>
 #include <cmath>
 
 #include "common.hpp"
+#include "norm_rope.hpp"
 
 namespace glt {
 
@@ -122,7 +124,34 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_scalar(const uint16_t* __rest
 }
 
 // Backward: dx = dy*r*w - x*mean(dy*x*w)*r^3 (reference
-// src/kernels_rmsnorm_kernels.inc:86-125). Lane L of wavefront q owns chunks
+// src/kernels_rmsnorm_kernels.inc:86-125). The per-chunk arithmetic (8
+// elements: x and w as bf16, dy and dx as f32) is shared by both backward
+// kernels, so they round alike.
+__device__ __forceinline__ float bwd_chunk_dot(const u32x4& xq, const u32x4& wq, const f32x4& d0, const f32x4& d1) {
+  float f[8], g[8];
+  unpack8(xq, f);
+  unpack8(wq, g);
+  float acc = 0.f;
+  acc += d0.x * f[0] * g[0] + d0.y * f[1] * g[1] + d0.z * f[2] * g[2] + d0.w * f[3] * g[3];
+  acc += d1.x * f[4] * g[4] + d1.y * f[5] * g[5] + d1.z * f[6] * g[6] + d1.w * f[7] * g[7];
+  return acc;
+}
+__device__ __forceinline__ void bwd_chunk_out(const u32x4& xq, const u32x4& wq, const f32x4& d0, const f32x4& d1,
+                                              float r, float mean, float r3, f32x4& o0, f32x4& o1) {
+  float f[8], g[8];
+  unpack8(xq, f);
+  unpack8(wq, g);
+  o0.x = d0.x * r * g[0] - f[0] * mean * r3;
+  o0.y = d0.y * r * g[1] - f[1] * mean * r3;
+  o0.z = d0.z * r * g[2] - f[2] * mean * r3;
+  o0.w = d0.w * r * g[3] - f[3] * mean * r3;
+  o1.x = d1.x * r * g[4] - f[4] * mean * r3;
+  o1.y = d1.y * r * g[5] - f[5] * mean * r3;
+  o1.z = d1.z * r * g[6] - f[6] * mean * r3;
+  o1.w = d1.w * r * g[7] - f[7] * mean * r3;
+}
+
+// Lane L of wavefront q owns chunks
 // q*64*NC + L + 64*i (8 elements: x as bf16, dy and dx as f32).
 template <int NC>
 __global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* __restrict__ dy,
@@ -155,13 +184,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* _
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = c0 + 64 * i;
-    if (c < nch) {
-      float f[8], g[8];
-      unpack8(xv[i], f);
-      unpack8(wv[i], g);
-      acc += d0[i].x * f[0] * g[0] + d0[i].y * f[1] * g[1] + d0[i].z * f[2] * g[2] + d0[i].w * f[3] * g[3];
-      acc += d1[i].x * f[4] * g[4] + d1[i].y * f[5] * g[5] + d1[i].z * f[6] * g[6] + d1[i].w * f[7] * g[7];
-    }
+    if (c < nch) acc += bwd_chunk_dot(xv[i], wv[i], d0[i], d1[i]);
   }
   const float mean = row_sum<kBwdWaves>(acc, part) / (float)D;
   f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * D);
@@ -169,23 +192,74 @@ __global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* _
   for (int i = 0; i < NC; ++i) {
     const int c = c0 + 64 * i;
     if (c < nch) {
-      float f[8], g[8];
-      unpack8(xv[i], f);
-      unpack8(wv[i], g);
       f32x4 o0, o1;
-      o0.x = d0[i].x * r * g[0] - f[0] * mean * r3;
-      o0.y = d0[i].y * r * g[1] - f[1] * mean * r3;
-      o0.z = d0[i].z * r * g[2] - f[2] * mean * r3;
-      o0.w = d0[i].w * r * g[3] - f[3] * mean * r3;
-      o1.x = d1[i].x * r * g[4] - f[4] * mean * r3;
-      o1.y = d1[i].y * r * g[5] - f[5] * mean * r3;
-      o1.z = d1[i].z * r * g[6] - f[6] * mean * r3;
-      o1.w = d1[i].w * r * g[7] - f[7] * mean * r3;
+      bwd_chunk_out(xv[i], wv[i], d0[i], d1[i], r, mean, r3, o0, o1);
       dxr[2 * c] = o0;
       dxr[2 * c + 1] = o1;
     }
   }
 }
+
+// The same backward, one wavefront per row, for a persistent grid that runs
+// beside another kernel on the CUs that kernel leaves idle (D/8 <= 512
+// chunks: the single-chunk layout of rmsnorm_bwd_vec). Lane L does the work
+// of lane L of each of the eight wavefronts of rmsnorm_bwd_vec<1> (chunk
+// 64 q + L for q = 0..7), reduces each of those partial sums across the
+// wavefront and adds the eight totals in order: the row's mean and dx are
+// bit-identical to rmsnorm_bwd_vec<1>'s. The weight row is loaded once.
+// Four wavefronts per workgroup (one per SIMD: the row's 24 KB of operands
+// stay in registers).
+constexpr int kRowsWaves = 4;
+__global__ void __launch_bounds__(64 * kRowsWaves) rmsnorm_bwd_rows_kernel(const float* __restrict__ dy, const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ w, const float* __restrict__ var,
+                                                        float* __restrict__ dx, int M, int D, float eps) {
+  constexpr int Q = kBwdWaves;  // the eight wavefronts of rmsnorm_bwd_vec<1>
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = D >> 3;
+  const u32x4* wr = reinterpret_cast<const u32x4*>(w);
+  u32x4 wv[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) wv[q] = 64 * q + lane < nch ? wr[64 * q + lane] : u32x4{0u, 0u, 0u, 0u};
+  for (int64_t row = (int64_t)blockIdx.x * kRowsWaves + wave; row < M; row += (int64_t)gridDim.x * kRowsWaves) {
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * D);
+    const f32x4* dyr = reinterpret_cast<const f32x4*>(dy + row * D);
+    u32x4 xv[Q];
+    f32x4 d0[Q], d1[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int c = 64 * q + lane;
+      if (c < nch) {
+        xv[q] = __builtin_nontemporal_load(xr + c);
+        d0[q] = dyr[2 * c];
+        d1[q] = dyr[2 * c + 1];
+      }
+    }
+    const float r = rsqrtf(var[row] + eps);
+    const float r3 = r * r * r;
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int c = 64 * q + lane;
+      float acc = 0.f;
+      if (c < nch) acc += bwd_chunk_dot(xv[q], wv[q], d0[q], d1[q]);
+      t += wave_sum(acc);
+    }
+    const float mean = t / (float)D;
+    f32x4* dxr = reinterpret_cast<f32x4*>(dx + row * D);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int c = 64 * q + lane;
+      if (c < nch) {
+        f32x4 o0, o1;
+        bwd_chunk_out(xv[q], wv[q], d0[q], d1[q], r, mean, r3, o0, o1);
+        dxr[2 * c] = o0;
+        dxr[2 * c + 1] = o1;
+      }
+    }
+  }
+}
+
+
 
 __global__ void __launch_bounds__(256) rmsnorm_bwd_scalar(const float* __restrict__ dy,
                                                           const uint16_t* __restrict__ x,
@@ -213,6 +287,34 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 static int lane_chunks(int D, int waves) {
   const int64_t ch = cdiv(cdiv(D / 8, 64), waves);
   return ch <= 1 ? 1 : ch <= 2 ? 2 : ch <= 4 ? 4 : ch <= 8 ? 8 : 0;
+}
+
+// LDS the row kernel asks for (it uses none): more than half of a CU's
+// 160 KB, so two of its workgroups never share a CU.
+constexpr int kRowsKernelLds = 96 * 1024;
+
+bool rmsnorm_bwd_rows_ok(const float* dy, const uint16_t* x, const uint16_t* w, const float* dx, int M, int D) {
+  return M > 0 && D > 0 && D % 8 == 0 && lane_chunks(D, kBwdWaves) == 1 && aligned16(x) && aligned16(w) &&
+         aligned16(dy) && aligned16(dx);
+}
+
+glt_status rmsnorm_bwd_rows(const float* dy, const uint16_t* x, const uint16_t* w, const float* var, float* dx, int M,
+                            int D, float eps, int grid, hipStream_t st) {
+  GLT_CHECK(rmsnorm_bwd_rows_ok(dy, x, w, dx, M, D) && grid > 0, GLT_ERR_UNSUPPORTED,
+            "rmsnorm_bwd_rows: M=%d D=%d grid=%d", M, D, grid);
+  static std::atomic<bool> attr_set[64];
+  int dev = 0;
+  GLT_TRY_HIP(hipGetDevice(&dev));
+  GLT_CHECK(dev >= 0 && dev < 64, GLT_ERR_HIP, "rmsnorm_bwd_rows: device index %d out of range", dev);
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
+    GLT_TRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(rmsnorm_bwd_rows_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kRowsKernelLds));
+    attr_set[dev].store(true, std::memory_order_release);
+  }
+  GLT_LAUNCH("rmsnorm_bwd_beside", rmsnorm_bwd_rows_kernel, dim3((unsigned)grid), dim3(64 * kRowsWaves), kRowsKernelLds, st,
+             dy, x, w, var, dx, M, D, eps);
+  GLT_LAUNCH_CHECK("rmsnorm_bwd_rows");
+  return GLT_OK;
 }
 
 // ------------------------------------------------------------------- RoPE

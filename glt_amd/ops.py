@@ -131,13 +131,20 @@ def mlp_backward_workspace(base, slices, M, N, explicit=True, recompute=False):
 
 
 def mlp_backward(base, slices, x, dy, N, gate_pre=None, up_pre=None, inter=None, want_dx=True, explicit=True,
-                 recompute=False, state=None, workspace=None):
+                 recompute=False, state=None, workspace=None, norm=None):
     """Graft-only backward (reference backward_layer FFN section,
     src/layer_backward_impl.inc:10-361). dy is [M,D] in the path dtype or
     f32 (the reference's upstream gradient, rounded once inside on the bf16
     path). Returns dx (f32) and per-slice [gate, up, down] f32 gradients in
-    [S,H] storage."""
+    [S,H] storage.
+
+    norm = (norm_x, norm_w, var, eps): x is the output of that RMSNorm
+    (reference rms_norm of the FFN input); the call then also runs its
+    backward on dx (glt_mlp_rmsnorm_bwd, beside the weight-gradient GEMM)
+    and returns (dx, grads, norm_dx)."""
     M = x.shape[0]
+    if norm is not None:
+        want_dx = True
     d, keep = _desc(base, slices, M, N, explicit, recompute, state, dy_f32=dy.dtype == torch.float32)
     nbytes = F.load().glt_mlp_bwd_workspace_size(ctypes.byref(d))
     if workspace is None or workspace.numel() < nbytes:
@@ -151,6 +158,13 @@ def mlp_backward(base, slices, x, dy, N, gate_pre=None, up_pre=None, inter=None,
         grads.append(row)
         garr[j] = F.GraftGrads(_p(row[0]), _p(row[1]), _p(row[2]))
     b = base.c_struct()
+    if norm is not None:
+        norm_x, norm_w, var, eps = norm
+        norm_dx = torch.empty((M, base.D), dtype=torch.float32, device=x.device)
+        F.call("glt_mlp_rmsnorm_bwd", ctypes.byref(d), ctypes.byref(b), _p(x), _p(dy), _p(gate_pre), _p(up_pre),
+               _p(inter), _p(dx), garr, _p(workspace), nbytes, _p(norm_x), _p(norm_w), _p(var), eps, _p(norm_dx),
+               _stream())
+        return dx, grads, norm_dx
     F.call("glt_mlp_bwd", ctypes.byref(d), ctypes.byref(b), _p(x), _p(dy), _p(gate_pre), _p(up_pre), _p(inter),
            _p(dx), garr, _p(workspace), nbytes, _stream())
     return dx, grads

@@ -240,6 +240,25 @@ glt_status glt_mlp_bwd(const glt_mlp_desc* d, const glt_base_weights* w,
                        const void* up_pre, const void* inter, float* dx,
                        const glt_graft_grads* grads, void* ws, size_t ws_bytes,
                        void* stream);
+/* The FFN backward followed by the backward of the RMSNorm that produced its
+ * input, as the reference's backward_layer runs them (graft-only FFN backward,
+ * src/layer_backward_impl.inc:34-361, then rms_norm_bwd of the FFN norm,
+ * src/kernels_rmsnorm_kernels.inc:70-126): glt_mlp_bwd(d, w, x, dy, gate_pre,
+ * up_pre, inter, dx, grads, ws, ws_bytes) then glt_rmsnorm_bwd(dx, norm_x,
+ * norm_w, norm_var, norm_dx, M, D, eps), with the same results bit for bit.
+ * x is the RMSNorm's output (the FFN input), norm_x its input (bf16 [M,D]),
+ * norm_w its weight [D], norm_var its saved mean squares [M]; dx (required)
+ * receives the FFN input gradient and norm_dx (f32 [M,D], may be dx) the
+ * norm input gradient. The RMSNorm backward runs on a per-device helper
+ * stream, on the CUs the weight-gradient GEMM leaves idle, joined to
+ * `stream` before the call's work on it ends. bf16 path only. */
+glt_status glt_mlp_rmsnorm_bwd(const glt_mlp_desc* d, const glt_base_weights* w,
+                               const void* x, const void* dy, const void* gate_pre,
+                               const void* up_pre, const void* inter, float* dx,
+                               const glt_graft_grads* grads, void* ws, size_t ws_bytes,
+                               const uint16_t* norm_x, const uint16_t* norm_w,
+                               const float* norm_var, float eps, float* norm_dx,
+                               void* stream);
 
 /* Unfused parity probes of the elementwise stages.
  * glt_silu_mul:  out = bf16(g*sigmoid(g)*u)   (reference fused_silu_product_kernel,

@@ -57,6 +57,22 @@ def test_host_validation_errors_without_gpu():
     assert lib.glt_adamw_step(1, 1, 1, 1, None, 10, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1.0, None, 0, None) == 5
 
 
+def test_mlp_rmsnorm_bwd_validation_without_gpu():
+    """The fused FFN + RMSNorm backward refuses a missing descriptor, a
+    missing dx or norm operand and the f32 path before any GPU call."""
+    from glt_amd import _ffi as F
+    lib = F.load()
+    desc = F.MlpDesc(16, 64, 64, 64, F.DTYPE_BF16, F.MLP_EXPLICIT, 0, None, None)
+    base = F.BaseWeights(16, 16, 16, None)
+    args = (ctypes.byref(base), 16, 16, 16, 16, 16)
+    tail = (None, None, 0)
+    assert lib.glt_mlp_rmsnorm_bwd(None, *args, 16, *tail, 16, 16, 16, 1e-5, 16, None) == 1
+    assert lib.glt_mlp_rmsnorm_bwd(ctypes.byref(desc), *args, None, *tail, 16, 16, 16, 1e-5, 16, None) == 1
+    assert lib.glt_mlp_rmsnorm_bwd(ctypes.byref(desc), *args, 16, *tail, 16, None, 16, 1e-5, 16, None) == 1
+    desc32 = F.MlpDesc(16, 64, 64, 64, F.DTYPE_F32, F.MLP_EXPLICIT, 0, None, None)
+    assert lib.glt_mlp_rmsnorm_bwd(ctypes.byref(desc32), *args, 16, *tail, 16, 16, 16, 1e-5, 16, None) == 3
+
+
 def test_eval_and_graft_adamw_validation_without_gpu():
     """glt_eval_stats and the graft AdamW step refuse bad requests, and pass
     an empty batch through, before any GPU call."""

@@ -413,3 +413,36 @@ def test_pipelined_adamw_stream_matches_sequential(dev):
                     (pip[0].gate, pip[0].up, pip[0].down, pip[1], pip[2], pip[0].packed)):
         assert torch.equal(bits(a), bits(b))
     assert torch.count_nonzero(ref[1]).item() > 0  # the step did update the moments
+
+
+@pytest.mark.parametrize("M,D,I,S,n_slices", [(2048, 1024, 2048, 256, 1),   # weight gradients leave CUs idle
+                                               (512, 512, 1024, 128, 0),     # no slices: no weight gradients
+                                               (512, 4608, 1024, 256, 1)])   # rows past 4096: not forked
+def test_mlp_rmsnorm_bwd_equals_the_two_calls(dev, M, D, I, S, n_slices):
+    """glt_mlp_rmsnorm_bwd (the FFN backward with the FFN norm's backward
+    beside its weight-gradient GEMM) gives glt_mlp_bwd's dx and gradients and
+    glt_rmsnorm_bwd's norm gradient bit for bit, whether or not the norm's
+    backward runs on the helper stream."""
+    import torch
+    from glt_amd import ops, synth
+    N = I + S
+    pl = [(I, S, 0, D)] if n_slices else []
+    wg, wu, wd, sl = make_layer(D, I, N, pl, True)
+    dt = torch.bfloat16
+    base = ops.BaseMLP(to_dev(wg, dt), to_dev(wu, dt), to_dev(wd, dt))
+    gs = [ops.GraftSlice(s["i0"], s["s"], s["h0"], s["h"], *(to_dev(s[p], torch.float32) for p in ("gate", "up", "down"))).pack()
+          for s in sl]
+    x_raw = to_dev(draw((M, D), 100, synth.TID_X, 0, 1, True), dt)
+    gamma = to_dev(draw((D,), 300, synth.TID_GAMMA, 1.0, 0.02, True), dt)
+    dy = to_dev(draw((M, D), 200, synth.TID_DY, 0, 1, False), torch.float32)
+    x, var = ops.rms_norm(x_raw, gamma, 1e-5)
+    y, gp, up, inter = ops.mlp_forward(base, gs, x, N)
+    dx0, g0 = ops.mlp_backward(base, gs, x, dy, N, gp, up, inter)
+    nd0 = ops.rms_norm_bwd(dx0, x_raw, gamma, var, 1e-5)
+    dx1, g1, nd1 = ops.mlp_backward(base, gs, x, dy, N, gp, up, inter, norm=(x_raw, gamma, var, 1e-5))
+    torch.cuda.synchronize()
+    assert torch.equal(dx0, dx1)
+    assert torch.equal(nd0, nd1)
+    for r0, r1 in zip(g0, g1):
+        for a, b in zip(r0, r1):
+            assert (a is None) == (b is None) and (a is None or torch.equal(a, b))
