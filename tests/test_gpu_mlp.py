@@ -446,3 +446,66 @@ def test_mlp_rmsnorm_bwd_equals_the_two_calls(dev, M, D, I, S, n_slices):
     for r0, r1 in zip(g0, g1):
         for a, b in zip(r0, r1):
             assert (a is None) == (b is None) and (a is None or torch.equal(a, b))
+
+
+def test_mlp_rmsnorm_bwd_in_a_graph(dev):
+    """glt_mlp_rmsnorm_bwd's fork onto the helper stream and its join are
+    captured with the caller's stream: a graph of the call, replayed three
+    times with eager work between the replays, reproduces the eager call's dx,
+    gradients and norm gradient bit for bit every time."""
+    import ctypes
+    import torch
+    from glt_amd import _ffi as F, ops, synth
+    M, D, I, S = 2048, 1024, 2048, 256
+    N = I + S
+    wg, wu, wd, sl = make_layer(D, I, N, [(I, S, 0, D)], True)
+    dt = torch.bfloat16
+    base = ops.BaseMLP(to_dev(wg, dt), to_dev(wu, dt), to_dev(wd, dt))
+    gsl = ops.GraftSlice(sl[0]["i0"], S, 0, D, *(to_dev(sl[0][p], torch.float32) for p in ("gate", "up", "down")))
+    gs = [gsl.pack()]
+    x_raw = to_dev(draw((M, D), 100, synth.TID_X, 0, 1, True), dt)
+    gamma = to_dev(draw((D,), 300, synth.TID_GAMMA, 1.0, 0.02, True), dt)
+    dy = to_dev(draw((M, D), 200, synth.TID_DY, 0, 1, False), torch.float32)
+    x, var = ops.rms_norm(x_raw, gamma, 1e-5)
+    y, gp, up, inter = ops.mlp_forward(base, gs, x, N)
+    dx_e, g_e, nd_e = ops.mlp_backward(base, gs, x, dy, N, gp, up, inter, norm=(x_raw, gamma, var, 1e-5))
+    torch.cuda.synchronize()
+
+    # the same call on preallocated buffers, captured
+    d, keep = ops._desc(base, gs, M, N, True, dy_f32=True)
+    nbytes = F.load().glt_mlp_bwd_workspace_size(ctypes.byref(d))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dx = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    nd = torch.empty_like(dx)
+    grads = [torch.empty((S, D), dtype=torch.float32, device="cuda") for _ in range(3)]
+    garr = (F.GraftGrads * 1)()
+    garr[0] = F.GraftGrads(*(t.data_ptr() for t in grads))
+    b = base.c_struct()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def call():
+        F.call("glt_mlp_rmsnorm_bwd", ctypes.byref(d), ctypes.byref(b), p(x), p(dy), p(gp), p(up), p(inter), p(dx),
+               garr, p(ws), nbytes, p(x_raw), p(gamma), p(var), 1e-5,
+               p(nd), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()   # first call sets per-device kernel attributes and creates the helper stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(3):
+        for t in (dx, nd, *grads):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dx, dx_e), rep
+        assert torch.equal(nd, nd_e), rep
+        for a, r in zip(grads, g_e[0]):
+            assert torch.equal(a, r), rep
+        _ = (x_raw.float() * 2).sum()   # eager work between replays
+        torch.cuda.synchronize()
