@@ -186,6 +186,20 @@ def test_config2_full_size_step_properties(dev):
         scale = full.abs().max().item()
         assert (summed - full).abs().max().item() <= 1e-5 * scale, p
 
+    # the backward with the FFN norm's backward beside the weight-gradient
+    # GEMM (192 tiles: the norm runs on the other CUs), as bench.py's step
+    # runs it: bit for bit the two separate calls
+    del parts
+    gamma = ops.fill_normal(torch.empty(D, dtype=torch.bfloat16, device="cuda"), 300, 12, 1.0, 0.02)
+    xn, var = ops.rms_norm(x, gamma, 1e-5)
+    dx2, g2 = ops.mlp_backward(base, slices, xn, dy, N, g, u, inter)
+    nd2 = ops.rms_norm_bwd(dx2, x, gamma, var, 1e-5)
+    dx3, g3, nd3 = ops.mlp_backward(base, slices, xn, dy, N, g, u, inter, norm=(x, gamma, var, 1e-5))
+    torch.cuda.synchronize()
+    assert torch.equal(dx2, dx3) and torch.equal(nd2, nd3)
+    for a, b in zip(g2[0], g3[0]):
+        assert torch.equal(a, b)
+
 
 def test_config5_decoder_layer_full_size(dev):
     """The decoder layer at its workload (2 x 4096 tokens, hidden 4096, 32
