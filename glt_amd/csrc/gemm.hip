@@ -1,6 +1,8 @@
 // Segment-list GEMM kernels: the gfx950 bf16 MFMA kernel and the strided
 // generic kernel (f32 path, unaligned shapes, graft-GEMM probes).
+#include <algorithm>
 #include <atomic>
+#include <cstdint>
 #include <cmath>
 
 #include "gemm.hpp"
@@ -861,10 +863,70 @@ int gemm_mfma_tiles(const GemmPlan& plan) {
   return tiles;
 }
 
+// Rows per launch (a multiple of kBM) for which every byte offset the MFMA
+// kernel forms from a problem's output, aux and A bases fits its 31-bit
+// buffer range; 0 if not even one tile of rows does.
+static int64_t mfma_row_block(const GemmPlan& plan) {
+  int64_t rows = INT64_MAX;
+  auto limit = [&](int64_t ld, int64_t esz) {
+    if (ld > 0) rows = std::min(rows, ((int64_t)kOob - 1) / (ld * esz) - kBM);
+  };
+  for (int p = 0; p < plan.args.nprob; ++p) {
+    const GProb& P = plan.args.p[p];
+    limit(P.ldo, P.out_f32 ? 4 : 2);
+    if (P.mode == EPI_DGDU) limit(P.ldaux, 2);
+    for (int i = P.seg0; i < P.seg0 + P.nseg; ++i) limit(plan.args.s[i].lda, 2);
+  }
+  return rows <= 0 ? 0 : rows / kBM * kBM;
+}
+
+// Rows [r0, r0 + rows) of every problem of plan, as a plan of their own
+// (output, aux and A bases moved to row r0).
+static GemmPlan mfma_rows(const GemmPlan& plan, int64_t r0, int64_t rows) {
+  GemmPlan sub = plan;
+  for (int p = 0; p < sub.args.nprob; ++p) {
+    GProb& P = sub.args.p[p];
+    const int64_t m = std::max<int64_t>(0, std::min<int64_t>(rows, (int64_t)P.M - r0));
+    if (m > 0) {
+      const int64_t eo = P.out_f32 ? 4 : 2;
+      auto mv = [&](void* q, int64_t ld, int64_t esz) {
+        return q ? static_cast<void*>(static_cast<char*>(q) + r0 * ld * esz) : nullptr;
+      };
+      P.out0 = mv(P.out0, P.ldo, eo);
+      P.out1 = mv(P.out1, P.ldo, eo);
+      P.out2 = mv(P.out2, P.ldo, eo);
+      P.aux0 = mv(const_cast<void*>(P.aux0), P.ldaux, 2);
+      P.aux1 = mv(const_cast<void*>(P.aux1), P.ldaux, 2);
+      for (int i = P.seg0; i < P.seg0 + P.nseg; ++i) {
+        GSeg& S = sub.args.s[i];
+        S.A = S.A ? static_cast<const char*>(S.A) + r0 * S.lda * 2 : nullptr;
+      }
+    }
+    P.M = (int)m;
+  }
+  return sub;
+}
+
 glt_status run_gemm(GemmPlan& plan, hipStream_t st, bool allow_mfma) {
   GArgs& a = plan.args;
   if (a.nprob == 0) return GLT_OK;
-  const bool mfma = allow_mfma && gemm_mfma_eligible(plan);
+  bool mfma = allow_mfma && gemm_mfma_eligible(plan);
+  if (allow_mfma && !mfma && plan.a_kind == LD_BF16 && plan.b_kind == LD_SHUF) {
+    // Too many rows for 31-bit offsets from the operand bases (e.g. an LM
+    // head of 16384 tokens x 128256 logits, 4 GiB of output): the MFMA
+    // kernel in row blocks whose offsets fit.
+    int64_t max_m = 0;
+    for (int p = 0; p < a.nprob; ++p) max_m = std::max<int64_t>(max_m, a.p[p].M);
+    const int64_t rows = mfma_row_block(plan);
+    if (rows >= kBM && rows < max_m && gemm_mfma_eligible(mfma_rows(plan, 0, rows))) {
+      for (int64_t r0 = 0; r0 < max_m; r0 += rows) {
+        GemmPlan sub = mfma_rows(plan, r0, rows);
+        const glt_status s = run_gemm(sub, st, true);
+        if (s != GLT_OK) return s;
+      }
+      return GLT_OK;
+    }
+  }
   const int bm = mfma ? kBM : 64;
   const int bn = mfma ? (plan.dual ? 128 : 256) : 64;
   const int mode = a.p[0].mode;

@@ -103,17 +103,6 @@ struct Proj {
   int64_t N;
   void* out;
 };
-// The MFMA kernel addresses a tile's rows through 31-bit buffer offsets
-// from the operand base, so a projection whose output (or input) extent
-// passes 2 GiB (an LM head over 16384 tokens x 128256 logits is 4 GiB) runs
-// as row blocks of at most this many tokens, each on the MFMA kernel.
-int64_t project_rows_per_launch(int64_t K, const Proj* ps, int n) {
-  int64_t widest = K;
-  for (int j = 0; j < n; ++j) widest = std::max(widest, ps[j].N);
-  const int64_t rows = ((int64_t)kOob - 1) / (widest * 2) - 256;  // one tile of rows past the block
-  return rows / 256 * 256;
-}
-
 glt_status project(const void* A, int64_t M, int64_t K, const Proj* ps, int n, int mode, const char* label,
                    hipStream_t st) {
   auto mfma_plan = [&](int64_t r0, int64_t rows, GemmPlan& plan) {
@@ -126,23 +115,13 @@ glt_status project(const void* A, int64_t M, int64_t K, const Proj* ps, int n, i
     }
   };
   {
+    // on the MFMA kernel, in row blocks when the output passes 31-bit
+    // offsets (run_gemm splits it)
     GemmPlan plan;
     mfma_plan(0, M, plan);
-    if (gemm_mfma_eligible(plan)) return run_gemm(plan, st);
-  }
-  const int64_t step = project_rows_per_launch(K, ps, n);
-  if (step >= 256 && M > step) {
-    GemmPlan first;
-    mfma_plan(0, step, first);
-    if (gemm_mfma_eligible(first)) {
-      for (int64_t r0 = 0; r0 < M; r0 += step) {
-        GemmPlan plan;
-        mfma_plan(r0, std::min(step, M - r0), plan);
-        const glt_status s = run_gemm(plan, st);
-        if (s != GLT_OK) return s;
-      }
-      return GLT_OK;
-    }
+    GemmPlan probe;
+    mfma_plan(0, std::min<int64_t>(M, 256), probe);
+    if (gemm_mfma_eligible(plan) || gemm_mfma_eligible(probe)) return run_gemm(plan, st);
   }
   GemmPlan gen;
   gen.label = label;

@@ -509,3 +509,33 @@ def test_mlp_rmsnorm_bwd_in_a_graph(dev):
             assert torch.equal(a, r), rep
         _ = (x_raw.float() * 2).sum()   # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_outputs_past_two_gib_split_into_row_blocks(dev):
+    """65536 tokens at N = 16384: the gate/up outputs and the dInter GEMM's
+    outputs and saved pre-activations pass 2 GiB, beyond the MFMA kernel's
+    31-bit buffer offsets, so run_gemm runs them as row blocks (65280 rows,
+    then 256). Token rows on both sides of the block boundary and at the
+    ends equal a call on just those tokens, bit for bit (every output row
+    depends on its own token only)."""
+    import torch
+    from glt_amd import ops, synth
+    M, D, I, S = 65536, 256, 16128, 256
+    N = I + S
+    wg, wu, wd, sl = make_layer(D, I, N, [(I, S, 0, D)], True)
+    dt = torch.bfloat16
+    base = ops.BaseMLP(to_dev(wg, dt), to_dev(wu, dt), to_dev(wd, dt))
+    gs = [ops.GraftSlice(sl[0]["i0"], S, 0, D, *(to_dev(sl[0][p], torch.float32) for p in ("gate", "up", "down"))).pack()]
+    x = ops.fill_normal(torch.empty((M, D), dtype=dt, device="cuda"), 100, 10, 0.0, 1.0)
+    dy = ops.fill_normal(torch.empty((M, D), dtype=dt, device="cuda"), 200, 11, 0.0, 1.0)
+    y, g, u, inter = ops.mlp_forward(base, gs, x, N)
+    dx, _ = ops.mlp_backward(base, gs, x, dy, N, g, u, inter)
+    torch.cuda.synchronize()
+    for r0 in (0, 65280 - 256, 65536 - 512):
+        rows = slice(r0, r0 + 512)
+        ys, gss, us, iss = ops.mlp_forward(base, gs, x[rows].contiguous(), N)
+        dxs, _ = ops.mlp_backward(base, gs, x[rows].contiguous(), dy[rows].contiguous(), N, gss, us, iss)
+        torch.cuda.synchronize()
+        for name, big, small in (("y", y, ys), ("gate_pre", g, gss), ("up_pre", u, us), ("inter", inter, iss)):
+            assert torch.equal(big[rows].view(torch.int16), small.view(torch.int16)), (name, r0)
+        assert torch.equal(dx[rows].view(torch.int32), dxs.view(torch.int32)), ("dx", r0)
