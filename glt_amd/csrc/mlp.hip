@@ -293,12 +293,19 @@ static glt_status fork_norm_bwd(const NormBwd& nb, const float* dx, int M, int D
   if (s != GLT_OK) return s;
   hipEvent_t ready = nullptr;
   GLT_TRY_HIP(hipEventCreateWithFlags(&ready, hipEventDisableTiming));
-  GLT_TRY_HIP(hipEventRecord(ready, st));
-  GLT_TRY_HIP(hipStreamWaitEvent(hs, ready, 0));
-  GLT_TRY_HIP(hipEventDestroy(ready));
+  hipError_t e = hipEventRecord(ready, st);
+  if (e == hipSuccess) e = hipStreamWaitEvent(hs, ready, 0);
+  const hipError_t de = hipEventDestroy(ready);
+  GLT_TRY_HIP(e);
+  GLT_TRY_HIP(de);
   if ((s = rmsnorm_bwd_rows(dx, nb.x, nb.w, nb.var, nb.dx, M, D, nb.eps, grid, hs)) != GLT_OK) return s;
   GLT_TRY_HIP(hipEventCreateWithFlags(done, hipEventDisableTiming));
-  GLT_TRY_HIP(hipEventRecord(*done, hs));
+  const hipError_t re = hipEventRecord(*done, hs);
+  if (re != hipSuccess) {
+    (void)hipEventDestroy(*done);
+    *done = nullptr;
+    GLT_TRY_HIP(re);
+  }
   return GLT_OK;
 }
 
@@ -501,13 +508,17 @@ static glt_status mlp_bwd_impl(const glt_mlp_desc* d, const glt_base_weights* w,
       const int idle = cus - gemm_mfma_tiles(plan);
       if (idle >= 16 && (s = fork_norm_bwd(*nb, dx, d->M, d->D, idle, st, &norm_ev)) != GLT_OK) return s;
     }
-    if ((s = run_gemm(plan, st)) != GLT_OK) return s;
+    // join the helper stream even when the GEMM launch failed, so that no
+    // work of this call is left running after it returns an error
+    const glt_status gs = run_gemm(plan, st);
     if (norm_ev) {
-      GLT_TRY_HIP(hipStreamWaitEvent(st, norm_ev, 0));
-      GLT_TRY_HIP(hipEventDestroy(norm_ev));
+      const hipError_t we = hipStreamWaitEvent(st, norm_ev, 0);
+      const hipError_t de = hipEventDestroy(norm_ev);
+      GLT_TRY_HIP(we);
+      GLT_TRY_HIP(de);
       *norm_done = true;
     }
-    return GLT_OK;
+    return gs;
   }
   // strided (generic) form: A(s, t) = src[t*N + i0 + s], B(h, t) = src2[t*D + h0 + h]
   GemmPlan plan;
