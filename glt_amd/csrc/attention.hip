@@ -39,6 +39,7 @@ constexpr int kStageBytes = 2 * kKBytes;     // K + V^T
 constexpr int kAttnLds = 2 * kStageBytes;    // 64 KB
 constexpr float kMaskVal = -1.0e30f;         // finite: no inf - inf
 constexpr float kSlack = 8.0f;               // running-max slack (log2 units)
+constexpr int kKPrefetch = 4;                // K fragments read ahead of their MFMA
 constexpr uint32_t kExtentA = 0x7FFFFFF0u;   // buffer extent below kOob
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -199,26 +200,25 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
     if (t < w_tiles) {
       const char* kt = smem + st * kStageBytes;
       const char* vt = kt + kKBytes;
-      // S^T blocks: keys 32kb + (8(e>>2) + 4lh + (e&3)), query lq
-      // four independent accumulation chains (two key blocks x two halves
-      // of d), merged after: a dependent MFMA waits for its predecessor
-      f32x16 sacc[2], spart[2][2];
+      // S^T blocks: keys 32kb + (8(e>>2) + 4lh + (e&3)), query lq. One
+      // accumulation chain per key block (the two alternate, and an MFMA
+      // accumulating onto its chain's previous result does not stall); the
+      // K fragment of step i + kKPrefetch is read before the MFMA of step i,
+      // which keeps the reads' LDS latency off the MFMA chain.
+      f32x16 sacc[2] = {f32x16{}, f32x16{}};
+      auto kread = [&](int i) {  // step i: key block i & 1, d 16(i >> 1) ..
+        const int r = 32 * (i & 1) + lq, c = 2 * (i >> 1) + lh;
+        return *reinterpret_cast<const bf16x8*>(kt + r * 256 + ((c ^ (r & 15)) << 4));
+      };
+      bf16x8 kq[kKPrefetch];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int i = 0; i < kKPrefetch; ++i) kq[i] = kread(i);
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) spart[kb][hf] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            const int r = 32 * kb + lq, c = 2 * (4 * hf + s) + lh;
-            const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + r * 256 + ((c ^ (r & 15)) << 4));
-            spart[kb][hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[4 * hf + s], spart[kb][hf], 0, 0, 0);
-          }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) sacc[kb] = spart[kb][0] + spart[kb][1];
+      for (int i = 0; i < 16; ++i) {
+        const bf16x8 kf = kq[i % kKPrefetch];
+        if (i + kKPrefetch < 16) kq[i % kKPrefetch] = kread(i + kKPrefetch);
+        sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[i >> 1], sacc[i & 1], 0, 0, 0);
+      }
       // Mask (only a tile that reaches past this wavefront's first query
       // or past T needs it): key index < lim, with lim the lane's causal /
       // sequence bound relative to this lane's first key of the tile.
