@@ -417,7 +417,8 @@ def test_pipelined_adamw_stream_matches_sequential(dev):
 
 @pytest.mark.parametrize("M,D,I,S,n_slices", [(2048, 1024, 2048, 256, 1),   # weight gradients leave CUs idle
                                                (512, 512, 1024, 128, 0),     # no slices: no weight gradients
-                                               (512, 4608, 1024, 256, 1)])   # rows past 4096: not forked
+                                               (512, 4608, 1024, 256, 1),    # rows past 4096: not forked
+                                               (1000, 1088, 1024, 128, 1)])  # 136 chunks per row: ragged lanes, ragged M
 def test_mlp_rmsnorm_bwd_equals_the_two_calls(dev, M, D, I, S, n_slices):
     """glt_mlp_rmsnorm_bwd (the FFN backward with the FFN norm's backward
     beside its weight-gradient GEMM) gives glt_mlp_bwd's dx and gradients and
