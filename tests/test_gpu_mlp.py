@@ -38,7 +38,8 @@ def _run(dev, D, I, N, pl, M, bf16, explicit=True, recompute=False, seed_x=100):
 
 @pytest.mark.parametrize("M,D,I,S", [(256, 256, 512, 128), (512, 512, 1024, 256)])
 def test_mfma_appended_bf16(dev, M, D, I, S):
-    """BASELINE's appended form (new neurons after the base rows) on the MFMA path."""
+    """The appended form (the graft slice's neurons after the base rows, as in the
+    benchmarked layer) on the MFMA path."""
     N = I + S
     r = _run(dev, D, I, N, [(I, S, 0, D)], M, bf16=True)
     for k, q in (("g", 2), ("u", 2), ("inter", 3), ("y", 4)):
