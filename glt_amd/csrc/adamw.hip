@@ -10,7 +10,7 @@
 namespace glt {
 
 
-constexpr int kClipBlocks = 1024;
+constexpr int kClipBlocks = 512;
 constexpr int kClipMaxSegs = 24;  // 3 projections x up to 8 slices
 
 // The gradient vectors one clip norm covers: partial sums of g^2 (f32, like
@@ -383,7 +383,7 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
 
 // ------------------------------------------------- the allocation-free step
 // glt_adamw_graft_step_noalloc keeps its clip partials in `scratch`, a
-// file-scope device array of kClipBlocks floats (4 KB) that every GPU the
+// file-scope device array of kClipBlocks floats (2 KB) that every GPU the
 // library runs on holds until the process ends. Host code never passes the
 // array's name to a kernel (on the host it is only a stand-in for the symbol):
 // the device address of each GPU's copy is looked up once per device with

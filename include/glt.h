@@ -419,11 +419,11 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
                                 size_t ws_bytes, void* stream);
 
 /* glt_adamw_graft_step without a workspace argument and without allocating:
- * the clip's partial sums live in a 4 KB device array of the library (one
+ * the clip's partial sums live in a 2 KB device array of the library (one
  * per GPU, held until the process ends). No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving or training loops). Every gradient size fits (the
- * clip uses at most 1024 partial sums); more than 8 slices are rejected as by
+ * clip uses at most 512 partial sums); more than 8 slices are rejected as by
  * glt_adamw_graft_step. Calls on one GPU share the array: calls that overlap
  * in time on one GPU (two streams) race; calls in stream order do not. */
 glt_status glt_adamw_graft_step_noalloc(const glt_graft_slice* slices, int32_t n_slices,
