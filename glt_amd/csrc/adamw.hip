@@ -11,18 +11,22 @@ namespace glt {
 
 
 constexpr int kClipBlocks = 512;
-constexpr int kClipMaxSegs = 24;  // 3 projections x up to 8 slices
+constexpr int kClipSegsPerLaunch = 32;
 
-// The gradient vectors one clip norm covers: partial sums of g^2 (f32, like
-// the reference reduce_l2_kernel, src/kernels_elementwise_impl.inc:141-165),
-// one partial per workgroup. Workgroup b covers elements
-// [(b - blk0[j]) * chunk, ...+chunk) of segment j, blk0[j] <= b < blk0[j+1].
+// The gradient vectors of one launch of the clip's partial sums: f32 sums of
+// g^2 (like the reference reduce_l2_kernel,
+// src/kernels_elementwise_impl.inc:141-165), one partial per workgroup.
+// Workgroup b covers elements [(b - blk0[j]) * chunk, ...+chunk) of segment
+// j, blk0[j] <= b < blk0[j+1], and writes partial[out0 + b]. One clip norm
+// may take several launches (any number of segments): they share one chunk
+// size and write consecutive ranges of the partials.
 struct ClipSegs {
-  const float* g[kClipMaxSegs];
-  int64_t n[kClipMaxSegs];
-  int blk0[kClipMaxSegs + 1];
+  const float* g[kClipSegsPerLaunch];
+  int64_t n[kClipSegsPerLaunch];
+  int blk0[kClipSegsPerLaunch + 1];
   int64_t chunk;  // elements per workgroup, a multiple of 1024
   int nseg;
+  int out0;
 };
 
 __global__ void __launch_bounds__(256) sumsq_partial_kernel(const ClipSegs segs, float* __restrict__ partial) {
@@ -54,7 +58,7 @@ __global__ void __launch_bounds__(256) sumsq_partial_kernel(const ClipSegs segs,
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
   __syncthreads();
-  if (threadIdx.x == 0) partial[b] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  if (threadIdx.x == 0) partial[segs.out0 + b] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
 }
 
 // scale = clip/norm if norm > clip else 1, norm = sqrt(sum + 1e-8)
@@ -73,32 +77,48 @@ __device__ float block_clip_scale(const float* __restrict__ partial, int np, flo
   return norm > clip ? clip / norm : 1.0f;
 }
 
-// The partials of a clip over segs: ws[0, np). Returns np through *np_out.
-glt_status launch_clip(const ClipSegs& segs_in, float* ws, size_t ws_floats, int* np_out, hipStream_t st) {
-  ClipSegs segs = segs_in;
+// The partials of one clip norm over the nseg gradient vectors g[j] of n[j]
+// elements: ws[0, np), from as many launches as the segments need
+// (kClipSegsPerLaunch each). The chunk is the smallest multiple of 1024 whose
+// workgroups over all segments number at most kClipBlocks, so each segment
+// needs at least one partial: at most kClipBlocks segments. Returns np
+// through *np_out.
+glt_status launch_clip(const float* const* g, const int64_t* n, int nseg, float* ws, size_t ws_floats, int* np_out,
+                       hipStream_t st) {
+  GLT_CHECK(nseg <= kClipBlocks, GLT_ERR_UNSUPPORTED,
+            "adamw clip: %d gradient segments, at most %d (one partial sum each)", nseg, kClipBlocks);
   int64_t total = 0;
-  for (int j = 0; j < segs.nseg; ++j) total += segs.n[j];
-  // the smallest chunk (a multiple of 1024) whose workgroups over all
-  // segments number at most kClipBlocks
+  for (int j = 0; j < nseg; ++j) total += n[j];
   int64_t chunk = std::max<int64_t>(1024, cdiv(cdiv(total, kClipBlocks), 1024) * 1024);
   auto blocks = [&](int64_t c) {
     int64_t nb = 0;
-    for (int j = 0; j < segs.nseg; ++j) nb += cdiv(segs.n[j], c);
+    for (int j = 0; j < nseg; ++j) nb += cdiv(n[j], c);
     return nb;
   };
   while (blocks(chunk) > kClipBlocks) chunk += 1024;
-  segs.chunk = chunk;
   int np = 0;
-  for (int j = 0; j < segs.nseg; ++j) {
-    segs.blk0[j] = np;
-    np += (int)cdiv(segs.n[j], chunk);
+  for (int j0 = 0; j0 < nseg; j0 += kClipSegsPerLaunch) {
+    ClipSegs segs{};
+    segs.chunk = chunk;
+    segs.out0 = np;
+    int nb = 0;
+    for (int j = j0; j < nseg && segs.nseg < kClipSegsPerLaunch; ++j) {
+      segs.g[segs.nseg] = g[j];
+      segs.n[segs.nseg] = n[j];
+      segs.blk0[segs.nseg] = nb;
+      nb += (int)cdiv(n[j], chunk);
+      ++segs.nseg;
+    }
+    segs.blk0[segs.nseg] = nb;
+    if (nb == 0) continue;  // every segment of this launch is empty
+    GLT_CHECK((size_t)(np + nb) <= ws_floats, GLT_ERR_WORKSPACE, "adamw clip: %d partial sums, room for %zu",
+              np + nb, ws_floats);
+    GLT_LAUNCH("clip_sumsq", sumsq_partial_kernel, dim3(nb), dim3(256), 0, st, segs, ws);
+    GLT_LAUNCH_CHECK("sumsq_partial");
+    np += nb;
   }
-  // nothing to sum (every segment empty): one workgroup writes a zero partial
-  if (np == 0) np = 1;
-  segs.blk0[segs.nseg] = np;
-  GLT_CHECK((size_t)np <= ws_floats, GLT_ERR_WORKSPACE, "adamw clip: %d partial sums, room for %zu", np, ws_floats);
-  GLT_LAUNCH("clip_sumsq", sumsq_partial_kernel, dim3(np), dim3(256), 0, st, segs, ws);
-  GLT_LAUNCH_CHECK("sumsq_partial");
+  // every segment empty: np = 0, and the update's scale comes from the
+  // norm of an empty sum
   *np_out = np;
   return GLT_OK;
 }
@@ -145,8 +165,10 @@ __global__ void __launch_bounds__(256) adamw_kernel(float* __restrict__ w, const
 // projection of a step in one launch: the f32 state streams through
 // registers as 16-byte accesses, the new weights go through LDS once, and
 // every mirror is written with 16-byte stores. The master is read once
-// instead of once per mirror.
-constexpr int kMaxPackJobs = kClipMaxSegs;
+// instead of once per mirror. One launch takes up to kMaxPackJobs
+// projections; a step over more issues several, which all read the same
+// clip partials.
+constexpr int kMaxPackJobs = 24;
 struct PackJob {
   float* w;
   const float* g;
@@ -271,11 +293,9 @@ glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* mirr
   if (clip_norm > 0.f) {
     GLT_CHECK(ws && ws_bytes >= glt_adamw_workspace_size(n), GLT_ERR_WORKSPACE,
               "glt_adamw_step: clip needs %zu workspace bytes", glt_adamw_workspace_size(n));
-    ClipSegs segs{};
-    segs.g[0] = g;
-    segs.n[0] = n;
-    segs.nseg = 1;
-    glt_status s = launch_clip(segs, static_cast<float*>(ws), ws_bytes / sizeof(float), &ci.np, st);
+    const float* gs[1] = {g};
+    const int64_t ns[1] = {n};
+    glt_status s = launch_clip(gs, ns, 1, static_cast<float*>(ws), ws_bytes / sizeof(float), &ci.np, st);
     if (s != GLT_OK) return s;
     ci.partial = static_cast<const float*>(ws);
   }
@@ -296,40 +316,54 @@ static glt_status graft_step(const glt_graft_slice* slices, int32_t n_slices, fl
                              float* const* v, uint16_t* const* packed_out, int32_t proj_mask, int32_t step, float lr,
                              float beta1, float beta2, float eps, float weight_decay, float clip_norm,
                              float* clip_ws, size_t clip_ws_floats, hipStream_t st) {
-  GLT_CHECK(n_slices >= 0 && n_slices <= kClipMaxSegs / 3, GLT_ERR_UNSUPPORTED,
-            "glt_adamw_graft_step: %d slices (max %d)", n_slices, kClipMaxSegs / 3);
+  GLT_CHECK(n_slices >= 0, GLT_ERR_SHAPE, "glt_adamw_graft_step: %d slices", n_slices);
   GLT_CHECK(n_slices == 0 || (slices && grads && m && v), GLT_ERR_INVALID_ARG, "glt_adamw_graft_step: null pointer");
   for (int j = 0; j < n_slices; ++j)
     GLT_CHECK(grads[j] && m[j] && v[j], GLT_ERR_INVALID_ARG, "glt_adamw_graft_step: null state of slice %d", j);
   ClipIn ci{nullptr, 0, clip_norm};
   if (clip_norm > 0.f) {
-    // the global L2 norm over every projection this step updates (the
-    // reference clips all of its L*3 deltas together, grafting.hip:1149-1164;
-    // the gradients of projections it does not graft stay zero)
-    ClipSegs segs{};
+    // one global L2 norm over every projection this step updates, of every
+    // slice (the reference clips all of its L*3 deltas together,
+    // grafting.hip:1149-1164; the gradients of projections it does not
+    // graft stay zero)
+    const float* gs[kClipBlocks];
+    int64_t ns[kClipBlocks];
+    int nseg = 0;
     for (int j = 0; j < n_slices; ++j) {
       const glt_graft_slice& sl = slices[j];
       const int64_t sh = (int64_t)sl.s * sl.h;
       const float* masters[3] = {sl.master_gate, sl.master_up, sl.master_down};
       for (int p = 0; p < 3; ++p) {
         if (!masters[p] || !(proj_mask & (1 << p))) continue;
-        segs.g[segs.nseg] = grads[j] + p * sh;
-        segs.n[segs.nseg] = sh;
-        ++segs.nseg;
+        GLT_CHECK(nseg < kClipBlocks, GLT_ERR_UNSUPPORTED,
+                  "glt_adamw_graft_step: the clip covers at most %d projections (slice %d)", kClipBlocks, j);
+        gs[nseg] = grads[j] + p * sh;
+        ns[nseg] = sh;
+        ++nseg;
       }
     }
-    if (segs.nseg > 0) {
-      glt_status s = launch_clip(segs, clip_ws, clip_ws_floats, &ci.np, st);
+    if (nseg > 0) {
+      glt_status s = launch_clip(gs, ns, nseg, clip_ws, clip_ws_floats, &ci.np, st);
       if (s != GLT_OK) return s;
       ci.partial = clip_ws;
     }
   }
   const float b1c = 1.0f / (1.0f - powf(beta1, (float)(step + 1)));
   const float b2c = 1.0f / (1.0f - powf(beta2, (float)(step + 1)));
-  // projections with whole 64 x 64 tiles and a packed mirror: one fused
-  // launch for all of them; the others one flat update and a repack each
+  // projections with whole 64 x 64 tiles and a packed mirror: fused
+  // launches of up to kMaxPackJobs projections; the others one flat update
+  // and a repack each
   PackJobs jobs{};
   int tiles = 0;
+  auto flush = [&]() -> glt_status {
+    if (jobs.n == 0) return GLT_OK;
+    GLT_LAUNCH("adamw_pack", adamw_pack_kernel, dim3((unsigned)tiles), dim3(256), 0, st, jobs, lr, beta1, beta2, b1c,
+               b2c, eps, weight_decay, ci);
+    GLT_LAUNCH_CHECK("adamw_pack");
+    jobs.n = 0;
+    tiles = 0;
+    return GLT_OK;
+  };
   for (int j = 0; j < n_slices; ++j) {
     const glt_graft_slice& sl = slices[j];
     const int64_t sh = (int64_t)sl.s * sl.h;
@@ -343,7 +377,11 @@ static glt_status graft_step(const glt_graft_slice* slices, int32_t n_slices, fl
       uint16_t* pk = packed_out ? packed_out[j] : nullptr;
       if (pk && sl.s % 64 == 0 && sl.h % 64 == 0 && al16(w) && al16(gp) && al16(mp) && al16(vp) && al16(pk)) {
         const int64_t t = sh / 4096;
-        GLT_CHECK(tiles + t < (1ll << 31), GLT_ERR_SHAPE, "glt_adamw_graft_step: %lld tiles", (long long)(tiles + t));
+        GLT_CHECK(t < (1ll << 31), GLT_ERR_SHAPE, "glt_adamw_graft_step: %lld tiles in one projection", (long long)t);
+        if (jobs.n == kMaxPackJobs || tiles + t >= (1ll << 31)) {
+          glt_status s = flush();
+          if (s != GLT_OK) return s;
+        }
         uint16_t* rm = pk + 2 * p * sh;
         jobs.j[jobs.n++] = PackJob{w, gp, mp, vp, rm, rm + sh, pk + packed_shuf_offset(sl.s, sl.h, 2 * p),
                                    pk + packed_shuf_offset(sl.s, sl.h, 2 * p + 1), sl.s, sl.h, tiles};
@@ -359,12 +397,7 @@ static glt_status graft_step(const glt_graft_slice* slices, int32_t n_slices, fl
       }
     }
   }
-  if (jobs.n > 0) {
-    GLT_LAUNCH("adamw_pack", adamw_pack_kernel, dim3((unsigned)tiles), dim3(256), 0, st, jobs, lr, beta1, beta2, b1c,
-               b2c, eps, weight_decay, ci);
-    GLT_LAUNCH_CHECK("adamw_pack");
-  }
-  return GLT_OK;
+  return flush();
 }
 }  // namespace glt
 

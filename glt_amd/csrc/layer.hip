@@ -419,8 +419,13 @@ __global__ void __launch_bounds__(256) eval_row_stats_kernel(const uint16_t* log
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       se += __expf(f[e] - m);
-      s += (double)f[e];
-      s2 += (double)(f[e] * f[e]);  // exact: a bf16 square fits in f32
+      // squared in f64 like the reference (static_cast<double>(f) * f): the
+      // f32 square of a large or tiny logit overflows or underflows; the
+      // product of two f32 values is exact in f64, so one fma is the
+      // reference's multiply and add
+      const double d = (double)f[e];
+      s += d;
+      s2 = __builtin_fma(d, d, s2);
     }
   };
   if ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && V % 8 == 0) {
@@ -443,8 +448,9 @@ __global__ void __launch_bounds__(256) eval_row_stats_kernel(const uint16_t* log
         m = f;
       }
       se += __expf(f - m);
-      s += (double)f;
-      s2 += (double)(f * f);
+      const double d = (double)f;
+      s += d;
+      s2 = __builtin_fma(d, d, s2);
     }
   }
 #pragma unroll

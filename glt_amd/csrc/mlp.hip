@@ -285,27 +285,36 @@ static glt_status helper_stream(hipStream_t& out) {
 // Starts the RMSNorm backward of dx on the helper stream once everything
 // enqueued on st so far is done, on `grid` persistent workgroups; *done is
 // recorded on the helper stream after it (the caller waits for it on st and
-// destroys it).
+// destroys it). Both events exist before the launch, so an error after it
+// can still be made to wait for the launched kernel: no work of the call is
+// left running once it has returned an error.
 static glt_status fork_norm_bwd(const NormBwd& nb, const float* dx, int M, int D, int grid, hipStream_t st,
                                 hipEvent_t* done) {
   hipStream_t hs = nullptr;
   glt_status s = helper_stream(hs);
   if (s != GLT_OK) return s;
-  hipEvent_t ready = nullptr;
+  hipEvent_t ready = nullptr, fin = nullptr;
   GLT_TRY_HIP(hipEventCreateWithFlags(&ready, hipEventDisableTiming));
-  hipError_t e = hipEventRecord(ready, st);
+  hipError_t e = hipEventCreateWithFlags(&fin, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(ready, st);
   if (e == hipSuccess) e = hipStreamWaitEvent(hs, ready, 0);
   const hipError_t de = hipEventDestroy(ready);
-  GLT_TRY_HIP(e);
-  GLT_TRY_HIP(de);
-  if ((s = rmsnorm_bwd_rows(dx, nb.x, nb.w, nb.var, nb.dx, M, D, nb.eps, grid, hs)) != GLT_OK) return s;
-  GLT_TRY_HIP(hipEventCreateWithFlags(done, hipEventDisableTiming));
-  const hipError_t re = hipEventRecord(*done, hs);
-  if (re != hipSuccess) {
-    (void)hipEventDestroy(*done);
-    *done = nullptr;
-    GLT_TRY_HIP(re);
+  if (e == hipSuccess) e = de;
+  if (e != hipSuccess) {
+    if (fin) (void)hipEventDestroy(fin);
+    GLT_TRY_HIP(e);
   }
+  s = rmsnorm_bwd_rows(dx, nb.x, nb.w, nb.var, nb.dx, M, D, nb.eps, grid, hs);
+  e = hipEventRecord(fin, hs);
+  if (s != GLT_OK || e != hipSuccess) {
+    // the kernel may have been enqueued: wait for the helper stream
+    const hipError_t se = hipStreamSynchronize(hs);
+    (void)hipEventDestroy(fin);
+    if (s != GLT_OK) return s;
+    GLT_TRY_HIP(e);
+    GLT_TRY_HIP(se);
+  }
+  *done = fin;
   return GLT_OK;
 }
 
@@ -512,7 +521,9 @@ static glt_status mlp_bwd_impl(const glt_mlp_desc* d, const glt_base_weights* w,
     // work of this call is left running after it returns an error
     const glt_status gs = run_gemm(plan, st);
     if (norm_ev) {
-      const hipError_t we = hipStreamWaitEvent(st, norm_ev, 0);
+      hipError_t we = hipStreamWaitEvent(st, norm_ev, 0);
+      // no join on st: wait for the helper stream's kernel on the host
+      if (we != hipSuccess) (void)hipEventSynchronize(norm_ev);
       const hipError_t de = hipEventDestroy(norm_ev);
       GLT_TRY_HIP(we);
       GLT_TRY_HIP(de);

@@ -153,12 +153,14 @@ __device__ __forceinline__ void bwd_chunk_out(const u32x4& xq, const u32x4& wq, 
 
 // Lane L of wavefront q owns chunks
 // q*64*NC + L + 64*i (8 elements: x as bf16, dy and dx as f32).
+// dy and dx may be the same buffer (an in-place backward): every store of a
+// row follows all loads of that row, so neither pointer is __restrict__.
 template <int NC>
-__global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* __restrict__ dy,
+__global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* dy,
                                                                  const uint16_t* __restrict__ x,
                                                                  const uint16_t* __restrict__ w,
                                                                  const float* __restrict__ var,
-                                                                 float* __restrict__ dx, int M, int D, float eps) {
+                                                                 float* dx, int M, int D, float eps) {
   __shared__ float part[kBwdWaves];
   const int lane = threadIdx.x & 63, c0 = (threadIdx.x >> 6) * 64 * NC + lane;
   const int64_t row = blockIdx.x;
@@ -210,9 +212,9 @@ __global__ void __launch_bounds__(64 * kBwdWaves) rmsnorm_bwd_vec(const float* _
 // Four wavefronts per workgroup (one per SIMD: the row's 24 KB of operands
 // stay in registers).
 constexpr int kRowsWaves = 4;
-__global__ void __launch_bounds__(64 * kRowsWaves) rmsnorm_bwd_rows_kernel(const float* __restrict__ dy, const uint16_t* __restrict__ x,
+__global__ void __launch_bounds__(64 * kRowsWaves) rmsnorm_bwd_rows_kernel(const float* dy, const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ w, const float* __restrict__ var,
-                                                        float* __restrict__ dx, int M, int D, float eps) {
+                                                        float* dx, int M, int D, float eps) {
   constexpr int Q = kBwdWaves;  // the eight wavefronts of rmsnorm_bwd_vec<1>
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = D >> 3;
@@ -261,11 +263,11 @@ __global__ void __launch_bounds__(64 * kRowsWaves) rmsnorm_bwd_rows_kernel(const
 
 
 
-__global__ void __launch_bounds__(256) rmsnorm_bwd_scalar(const float* __restrict__ dy,
+__global__ void __launch_bounds__(256) rmsnorm_bwd_scalar(const float* dy,
                                                           const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
                                                           const float* __restrict__ var,
-                                                          float* __restrict__ dx, int M, int D,
+                                                          float* dx, int M, int D,
                                                           float eps) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);

@@ -131,7 +131,7 @@ def mlp_backward_workspace(base, slices, M, N, explicit=True, recompute=False):
 
 
 def mlp_backward(base, slices, x, dy, N, gate_pre=None, up_pre=None, inter=None, want_dx=True, explicit=True,
-                 recompute=False, state=None, workspace=None, norm=None):
+                 recompute=False, state=None, workspace=None, norm=None, norm_in_place=False):
     """Graft-only backward (reference backward_layer FFN section,
     src/layer_backward_impl.inc:10-361). dy is [M,D] in the path dtype or
     f32 (the reference's upstream gradient, rounded once inside on the bf16
@@ -141,7 +141,8 @@ def mlp_backward(base, slices, x, dy, N, gate_pre=None, up_pre=None, inter=None,
     norm = (norm_x, norm_w, var, eps): x is the output of that RMSNorm
     (reference rms_norm of the FFN input); the call then also runs its
     backward on dx (glt_mlp_rmsnorm_bwd, beside the weight-gradient GEMM)
-    and returns (dx, grads, norm_dx)."""
+    and returns (dx, grads, norm_dx); norm_in_place writes norm_dx over dx
+    (the same tensor is returned twice)."""
     M = x.shape[0]
     if norm is not None:
         want_dx = True
@@ -160,7 +161,7 @@ def mlp_backward(base, slices, x, dy, N, gate_pre=None, up_pre=None, inter=None,
     b = base.c_struct()
     if norm is not None:
         norm_x, norm_w, var, eps = norm
-        norm_dx = torch.empty((M, base.D), dtype=torch.float32, device=x.device)
+        norm_dx = dx if norm_in_place else torch.empty((M, base.D), dtype=torch.float32, device=x.device)
         F.call("glt_mlp_rmsnorm_bwd", ctypes.byref(d), ctypes.byref(b), _p(x), _p(dy), _p(gate_pre), _p(up_pre),
                _p(inter), _p(dx), garr, _p(workspace), nbytes, _p(norm_x), _p(norm_w), _p(var), eps, _p(norm_dx),
                _stream())
@@ -186,10 +187,11 @@ def rms_norm(x, w, eps):
     return y, var
 
 
-def rms_norm_bwd(dy, x, w, var, eps):
-    """Reference rms_norm_bwd (grafting.hip:153-172); dy f32, returns dx f32."""
+def rms_norm_bwd(dy, x, w, var, eps, out=None):
+    """Reference rms_norm_bwd (grafting.hip:153-172); dy f32, returns dx f32
+    (into out when given, which may be dy itself)."""
     M, D = x.shape
-    dx = torch.empty((M, D), dtype=torch.float32, device=x.device)
+    dx = torch.empty((M, D), dtype=torch.float32, device=x.device) if out is None else out
     F.call("glt_rmsnorm_bwd", _p(dy), _p(x), _p(w), _p(var), _p(dx), M, D, eps, _stream())
     return dx
 

@@ -410,7 +410,9 @@ glt_status glt_adamw_step(float* w, float* g, float* m, float* v, uint16_t* bf16
  * projection the step updates, all slices together (the reference's
  * per-step clip over all of its deltas, grafting.hip:1149-1164, default
  * 1.0, src/config.hpp:85); it needs ws of glt_adamw_workspace_size(0)
- * bytes. At most 8 slices per call. */
+ * bytes. Any number of slices; with the clip on, the norm covers at most
+ * 512 projections (170 slices of gate, up and down), more return
+ * GLT_ERR_UNSUPPORTED. */
 glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
                                 float* const* grads, float* const* m, float* const* v,
                                 uint16_t* const* packed_out, int32_t proj_mask,
@@ -423,8 +425,8 @@ glt_status glt_adamw_graft_step(const glt_graft_slice* slices, int32_t n_slices,
  * per GPU, held until the process ends). No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving or training loops). Every gradient size fits (the
- * clip uses at most 512 partial sums); more than 8 slices are rejected as by
- * glt_adamw_graft_step. Calls on one GPU share the array: calls that overlap
+ * clip uses at most 512 partial sums), and so does every slice count
+ * glt_adamw_graft_step takes. Calls on one GPU share the array: calls that overlap
  * in time on one GPU (two streams) race; calls in stream order do not. */
 glt_status glt_adamw_graft_step_noalloc(const glt_graft_slice* slices, int32_t n_slices,
                                         float* const* grads, float* const* m, float* const* v,

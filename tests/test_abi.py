@@ -87,12 +87,18 @@ def test_eval_and_graft_adamw_validation_without_gpu():
     # chain over an empty batch), nothing counted
     assert lib.glt_eval_stats(None, 8, None, 0, 2, 8, 0, h, ctypes.byref(res), None, 0, None) == 0
     assert res.logits_hash == h and res.count == 0 and res.total_nll == 0.0
-    # graft AdamW: 9 slices are more than one call's clip takes (either form);
-    # the clip without its workspace
-    sl = (F.GraftSlice * 9)()
-    arr = F.ptr_array([16] * 9)
-    args = (sl, 9, arr, arr, arr, None, 7, 0, 1e-4, 0.9, 0.999, 1e-8, 0.01)
-    assert lib.glt_adamw_graft_step(*args, 0.0, None, 0, None) == 9
-    assert lib.glt_adamw_graft_step_noalloc(*args, 0.0, None) == 9
+    # graft AdamW: a negative slice count (either form); a clip over more
+    # projections than it has partial sums (171 slices x 3 > 512), refused
+    # before any launch; the clip without its workspace
+    sl = (F.GraftSlice * 171)()
+    for j in range(171):
+        sl[j].s, sl[j].h = 64, 64
+        sl[j].master_gate = sl[j].master_up = sl[j].master_down = 4096
+    arr = F.ptr_array([4096] * 171)
+    args = (sl, -1, arr, arr, arr, None, 7, 0, 1e-4, 0.9, 0.999, 1e-8, 0.01)
+    assert lib.glt_adamw_graft_step(*args, 0.0, None, 0, None) == 2
+    assert lib.glt_adamw_graft_step_noalloc(*args, 0.0, None) == 2
+    assert lib.glt_adamw_graft_step(sl, 171, arr, arr, arr, None, 7, 0, 1e-4, 0.9, 0.999, 1e-8, 0.01, 1.0,
+                                    ctypes.c_void_p(4096), 1 << 20, None) == 9
     assert lib.glt_adamw_graft_step(sl, 1, arr, arr, arr, None, 7, 0, 1e-4, 0.9, 0.999, 1e-8, 0.01, 1.0, None, 0,
                                     None) == 5

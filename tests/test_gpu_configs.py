@@ -166,7 +166,7 @@ def test_config2_full_size_step_properties(dev):
             assert abs(got - terms.sum()) <= 1e-4 * np.abs(terms).sum() + 1e-6, ("dW_down", s, hh, got, terms.sum())
             terms = dg * xf[:, hh]
             got = float(grads[0][0][s, hh])
-            assert abs(got - terms.sum()) <= 1e-2 * np.abs(terms).sum() + 1e-6, ("dW_gate", s, hh, got, terms.sum())
+            assert abs(got - terms.sum()) <= 1e-3 * np.abs(terms).sum() + 1e-6, ("dW_gate", s, hh, got, terms.sum())
     del dyf, xf
 
     # linearity over tokens
@@ -290,7 +290,7 @@ def test_config5_decoder_layer_full_size(dev):
             assert abs(got - terms.sum()) <= 1e-4 * np.abs(terms).sum() + 1e-6, ("dW_down", s_, hh, got)
             terms = dgc * xf[:, hh]
             got = float(grads[0][0][s_, hh])
-            assert abs(got - terms.sum()) <= 1e-2 * np.abs(terms).sum() + 1e-6, ("dW_gate", s_, hh, got)
+            assert abs(got - terms.sum()) <= 1e-3 * np.abs(terms).sum() + 1e-6, ("dW_gate", s_, hh, got)
     del dyb, xf, g, u, inter
 
     # the two sequences separately
@@ -305,3 +305,61 @@ def test_config5_decoder_layer_full_size(dev):
         full = grads[0][p].double()
         summed = parts[0][0][p].double() + parts[1][0][p].double()
         assert (summed - full).abs().max().item() <= 1e-5 * full.abs().max().item(), p
+
+
+def test_config2_adamw_clip_full_size(dev):
+    """The measured step's optimizer leg at its size: one appended slice of
+    S 1024 x H 4096 (3 x 4,194,304 = 12,582,912 gradients, so the clip's
+    partial sums run with a 25,600-element chunk over 492 workgroups, every
+    16-byte load of their unrolled loops live, and the update sums 492
+    partials) with the reference's clip 1.0 (grafting.hip:1149-1172,
+    src/kernels_optimizer_impl.inc:11-77), over steps 0 and 1. The workspace
+    form is checked against the oracle's clipped AdamW over the concatenated
+    gradients, the allocation-free form against it bit for bit, and every
+    orientation of the packed mirror against the new masters bit for bit."""
+    import torch
+    from glt_amd import _ffi as F
+    from glt_amd import ops
+    from helpers import assert_f32_close, packed_views, shuffle_b
+    S, H = 1024, D
+    n = 3 * S * H
+    a = _slices(torch, ops, [(I, S, 0, H)], seeds=(1,))
+    b = [ops.GraftSlice(s.i_start, s.s, s.h_start, s.h, s.gate.clone(), s.up.clone(), s.down.clone()) for s in a]
+    for sa, sb in zip(a, b):
+        sb.packed.copy_(sa.packed)
+    ma, va = torch.zeros(n, device=dev), torch.zeros(n, device=dev)
+    mb, vb = torch.zeros(n, device=dev), torch.zeros(n, device=dev)
+    w = np.concatenate([to_np(t).ravel() for t in (a[0].gate, a[0].up, a[0].down)])
+    rm = np.zeros(n, np.float32)
+    rv = np.zeros(n, np.float32)
+    ws_bytes = F.load().glt_adamw_workspace_size(0)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    lr, clip = 1e-4, 1.0
+    for step in (0, 1):
+        print("config-2 AdamW step", step, flush=True)
+        g = ops.fill_normal(torch.empty(n, dtype=torch.float32, device=dev), 400 + step, 1, 0.0, 0.01)
+        ops.adamw_graft_step(a, [g], [ma], [va], step, lr, clip_norm=clip, workspace=ws)
+        F.call("glt_adamw_graft_step_noalloc", ops._slices_array(b), 1, F.ptr_array([g.data_ptr()]),
+               F.ptr_array([mb.data_ptr()]), F.ptr_array([vb.data_ptr()]), F.ptr_array([b[0].packed.data_ptr()]),
+               7, step, lr, 0.9, 0.999, 1e-8, 0.01, clip, ops._stream())
+        torch.cuda.synchronize()
+        gn = to_np(g)
+        assert O.lib().orc_clip_scale(O._fp(gn), n, clip) < 0.05     # norm ~ 35: the clip acts
+        w, rm, rv = O.adamw(w, gn, rm, rv, step, lr, 0.9, 0.999, 1e-8, 0.01, clip_norm=clip)
+        got = np.concatenate([to_np(t).ravel() for t in (a[0].gate, a[0].up, a[0].down)])
+        assert_f32_close(got, w, tol=1e-6, what=f"w step {step}")
+        assert_f32_close(to_np(ma), rm, tol=1e-5, what=f"m step {step}")
+        assert_f32_close(to_np(va), rv, tol=1e-5, what=f"v step {step}")
+        i32 = lambda t: t.view(torch.int32)
+        for x, y in ((a[0].gate, b[0].gate), (a[0].up, b[0].up), (a[0].down, b[0].down), (ma, mb), (va, vb)):
+            assert torch.equal(i32(x), i32(y))
+        assert torch.equal(a[0].packed.view(torch.int16), b[0].packed.view(torch.int16))
+        bits = a[0].packed.view(torch.int16).cpu().numpy().view(np.uint16)
+        rowmajor, shuf = packed_views(O.bf16_bits_to_f32(bits), S, H)
+        for p, t in enumerate((a[0].gate, a[0].up, a[0].down)):
+            wb = O.bf16_round(to_np(t))
+            np.testing.assert_array_equal(rowmajor[2 * p], wb)
+            np.testing.assert_array_equal(rowmajor[2 * p + 1], wb.T)
+            np.testing.assert_array_equal(shuf[2 * p], shuffle_b(wb))
+            np.testing.assert_array_equal(shuf[2 * p + 1], shuffle_b(wb.T))
+        del g, bits, rowmajor, shuf

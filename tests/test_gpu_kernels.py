@@ -337,6 +337,62 @@ def test_adamw_graft_step_global_clip(dev, clip):
         np.testing.assert_array_equal(rowmajor[0], O.bf16_round(to_np(sl.gate)))
 
 
+@pytest.mark.parametrize("proj_mask", [7, 5])
+def test_adamw_graft_step_clip_over_36_slices(dev, proj_mask):
+    """One global clip over a whole model's graft: 36 slices (one per layer
+    at the reference's 36 layers, grafting.hip:1149-1164 clips all L*3 deltas
+    with one norm), more projections than one launch of the clip's partial
+    sums or of the fused update takes, mixing the fused-mirror shape with
+    the separate-pass one, against the oracle's clipped AdamW over the
+    concatenated gradients of every updated projection. proj_mask 5 leaves
+    the up projections out of the norm and untouched
+    (src/kernels_optimizer_impl.inc:20-25)."""
+    import torch
+    from glt_amd import ops
+    L = 36
+    shapes = [(64, 96) if j % 5 == 4 else (64, 128) for j in range(L)]
+    slices, grads, ms, vs, w0, gs = [], [], [], [], [], []
+    for j, (S, H) in enumerate(shapes):
+        masters = [torch.from_numpy(draw((S, H), 100 + j, p, 0, 0.02, bf16=False)).cuda() for p in range(3)]
+        w0.append([to_np(t).copy() for t in masters])
+        slices.append(ops.GraftSlice(0, S, 0, H, *masters).pack())
+        g = draw((3 * S * H,), 200 + j, 1, 0, 0.01, bf16=False)
+        gs.append(g.reshape(3, S * H))
+        grads.append(torch.from_numpy(g).cuda())
+        ms.append(torch.zeros(3 * S * H, device=dev))
+        vs.append(torch.zeros(3 * S * H, device=dev))
+    packed0 = [s.packed.clone() for s in slices]
+    ops.adamw_graft_step(slices, grads, ms, vs, 1, 1e-3, proj_mask=proj_mask, clip_norm=1.0)
+    torch.cuda.synchronize()
+    upd = [p for p in range(3) if proj_mask & (1 << p)]
+    allg = np.concatenate([gs[j][p] for j in range(L) for p in upd])
+    allw = np.concatenate([w0[j][p].ravel() for j in range(L) for p in upd])
+    z = np.zeros_like(allw)
+    assert O.lib().orc_clip_scale(O._fp(allg), allg.size, 1.0) < 0.5   # the clip acts
+    rw, rm, rv = O.adamw(allw, allg, z, z, 1, 1e-3, 0.9, 0.999, 1e-8, 0.01, clip_norm=1.0)
+    cat = lambda per: np.concatenate([per(j, p) for j in range(L) for p in upd])
+    got_w = cat(lambda j, p: to_np((slices[j].gate, slices[j].up, slices[j].down)[p]).ravel())
+    sh = lambda j: shapes[j][0] * shapes[j][1]
+    got_m = cat(lambda j, p: to_np(ms[j])[p * sh(j):(p + 1) * sh(j)])
+    got_v = cat(lambda j, p: to_np(vs[j])[p * sh(j):(p + 1) * sh(j)])
+    assert_f32_close(got_w, rw, tol=1e-6, what="w")
+    assert_f32_close(got_m, rm, tol=1e-5, what="m")
+    assert_f32_close(got_v, rv, tol=1e-5, what="v")
+    for j, sl in enumerate(slices):
+        rowmajor, shuf = packed_views(O.bf16_bits_to_f32(_bits(sl.packed)), sl.s, sl.h)
+        rowmajor0, shuf0 = packed_views(O.bf16_bits_to_f32(_bits(packed0[j])), sl.s, sl.h)
+        for p, t in enumerate((sl.gate, sl.up, sl.down)):
+            if p in upd:
+                wb = O.bf16_round(to_np(t))
+                np.testing.assert_array_equal(rowmajor[2 * p], wb)
+                np.testing.assert_array_equal(shuf[2 * p + 1], shuffle_b(wb.T))
+            else:   # skipped projection: master, moments and mirror untouched
+                np.testing.assert_array_equal(to_np(t), w0[j][p])
+                assert not to_np(ms[j])[p * sh(j):(p + 1) * sh(j)].any()
+                np.testing.assert_array_equal(rowmajor[2 * p], rowmajor0[2 * p])
+                np.testing.assert_array_equal(shuf[2 * p], shuf0[2 * p])
+
+
 def test_base_prepare_layout(dev):
     """The prepared base holds gate, up, down, down^T, gate^T, up^T in the
     fragment layout, bit for bit (ragged sizes pad with zeros)."""

@@ -424,7 +424,8 @@ def test_mlp_rmsnorm_bwd_equals_the_two_calls(dev, M, D, I, S, n_slices):
     """glt_mlp_rmsnorm_bwd (the FFN backward with the FFN norm's backward
     beside its weight-gradient GEMM) gives glt_mlp_bwd's dx and gradients and
     glt_rmsnorm_bwd's norm gradient bit for bit, whether or not the norm's
-    backward runs on the helper stream."""
+    backward runs on the helper stream; and so do both calls with the norm's
+    gradient written in place over their input gradient."""
     import torch
     from glt_amd import ops, synth
     N = I + S
@@ -447,6 +448,16 @@ def test_mlp_rmsnorm_bwd_equals_the_two_calls(dev, M, D, I, S, n_slices):
     assert torch.equal(nd0, nd1)
     for r0, r1 in zip(g0, g1):
         for a, b in zip(r0, r1):
+            assert (a is None) == (b is None) and (a is None or torch.equal(a, b))
+    # in place: norm_dx == dx
+    dx2, g2, nd2 = ops.mlp_backward(base, gs, x, dy, N, gp, up, inter, norm=(x_raw, gamma, var, 1e-5),
+                                    norm_in_place=True)
+    nd3 = dx0.clone()
+    ops.rms_norm_bwd(nd3, x_raw, gamma, var, 1e-5, out=nd3)
+    torch.cuda.synchronize()
+    assert nd2 is dx2 and torch.equal(nd2, nd0) and torch.equal(nd3, nd0)
+    for r0, r2 in zip(g0, g2):
+        for a, b in zip(r0, r2):
             assert (a is None) == (b is None) and (a is None or torch.equal(a, b))
 
 

@@ -71,20 +71,29 @@ def test_model_forward_matches_oracle(dev, explicit):
     assert_bf16_budget(to_np(logits), ref, q=8, what="logits")
 
 
-@pytest.mark.parametrize("reference_hash", [True, False])
-def test_eval_stats_match_oracle(dev, reference_hash):
+@pytest.mark.parametrize("reference_hash,extreme", [(True, False), (False, False), (True, True), (False, True)])
+def test_eval_stats_match_oracle(dev, reference_hash, extreme):
+    """extreme: logits of magnitude 2^70 and 2^-70, whose f32 squares overflow
+    and underflow; the sum of squares is formed in f64 as the reference's
+    (grafting.hip:525-547)."""
     import torch
     from glt_amd import ops
     B, T, V = 2, 33, 1500
     x = O.bf16_round(np.random.default_rng(8).normal(0, 3, (B * T, V)).astype(np.float32))
+    if extreme:
+        x[5, 17], x[40, 3], x[41, 1499] = 2.0 ** 70, -(2.0 ** 70), 2.0 ** -70
+        x[60, :] = 2.0 ** -70
     ids = np.random.default_rng(9).integers(0, V, (B, T)).astype(np.int32)
     r = ops.eval_stats(to_dev(x, torch.bfloat16), torch.tensor(ids).cuda(), reference_hash=reference_hash)
     ref = O.eval_stats(x.reshape(B, T, V), ids, reference_hash=reference_hash)
     assert r["logits_hash"] == ref["logits_hash"]
     assert r["count"] == ref["count"]
     assert r["total_nll"] == pytest.approx(ref["total_nll"], rel=1e-5)
-    assert r["logits_sum"] == pytest.approx(ref["logits_sum"], rel=1e-9, abs=1e-6)
+    # +-2^70 cancel in the sum: any f64 summation order loses up to a few of
+    # their ulps (2^18) there
+    assert r["logits_sum"] == pytest.approx(ref["logits_sum"], rel=1e-9, abs=2.0 ** 20 if extreme else 1e-6)
     assert r["logits_sumsq"] == pytest.approx(ref["logits_sumsq"], rel=1e-12)
+    assert np.isfinite(r["logits_sumsq"])
 
 
 @pytest.mark.parametrize("B,T,V,ld", [(2, 3, 128256, 128256),   # the Llama-3 vocabulary, 16-byte chunks

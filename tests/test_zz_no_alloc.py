@@ -68,3 +68,91 @@ def test_noalloc_graft_step_matches_workspace_form(dev):
         _call(F, ops, "glt_adamw_graft_step", c, step, 0.0, (None, 0))
         torch.cuda.synchronize()
         assert not torch.equal(c[2][0], b[2][0])
+
+
+def test_noalloc_graft_step_many_slices(dev):
+    """More slices than one launch of the clip or of the fused update takes
+    (12 slices, 36 projections, one clip norm over all of them): the
+    allocation-free form against the workspace form bit for bit."""
+    import torch
+    from glt_amd import _ffi as F
+    from glt_amd import ops
+    ws_bytes = F.load().glt_adamw_workspace_size(0)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    shapes = [(64, 128)] * 11 + [(64, 96)]
+    a = _state(torch, ops, shapes, 80)
+    b = _clone(torch, ops, a)
+    _call(F, ops, "glt_adamw_graft_step", a, 2, 1.0, (ctypes.c_void_p(ws.data_ptr()), ws_bytes))
+    _call(F, ops, "glt_adamw_graft_step_noalloc", b, 2, 1.0, ())
+    torch.cuda.synchronize()
+    bits = lambda t: t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)
+    for sa, sb in zip(a[0], b[0]):
+        for x, y in ((sa.gate, sb.gate), (sa.up, sb.up), (sa.down, sb.down), (sa.packed, sb.packed)):
+            assert torch.equal(bits(x), bits(y))
+    for xs, ys in ((a[2], b[2]), (a[3], b[3])):
+        for x, y in zip(xs, ys):
+            assert torch.equal(bits(x), bits(y))
+
+
+def test_noalloc_graft_step_in_a_hip_graph(dev):
+    """The allocation-free step captured in a HIP graph (its scratch address
+    baked into the captured launches) and replayed twice, with eager work
+    and synchronizations between the replays: each replay equals the eager
+    call on a copy of the same state bit for bit."""
+    import torch
+    from glt_amd import _ffi as F
+    from glt_amd import ops
+    shapes = [(128, 256), (64, 96)]
+    a = _state(torch, ops, shapes, 90)
+    b = _clone(torch, ops, a)
+    _call(F, ops, "glt_adamw_graft_step_noalloc", a, 5, 0.5, ())     # first call: the scratch lookup
+    _call(F, ops, "glt_adamw_graft_step_noalloc", b, 5, 0.5, ())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _call(F, ops, "glt_adamw_graft_step_noalloc", a, 5, 0.5, ())
+    torch.cuda.synchronize()
+    bits = lambda t: t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)
+    for rep in range(2):
+        print("noalloc graph replay", rep, flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        _call(F, ops, "glt_adamw_graft_step_noalloc", b, 5, 0.5, ())     # eager, on the copy
+        torch.cuda.synchronize()
+        for sa, sb in zip(a[0], b[0]):
+            for x, y in ((sa.gate, sb.gate), (sa.up, sb.up), (sa.down, sb.down), (sa.packed, sb.packed)):
+                assert torch.equal(bits(x), bits(y)), rep
+        for xs, ys in ((a[2], b[2]), (a[3], b[3])):
+            for x, y in zip(xs, ys):
+                assert torch.equal(bits(x), bits(y)), rep
+    del graph
+
+
+_FRESH = r"""
+import ctypes, sys, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+from glt_amd import _ffi as F
+from glt_amd import ops
+import test_zz_no_alloc as T
+st = T._state(torch, ops, [(128, 256), (64, 96)], 70)
+torch.cuda.synchronize()
+free0 = torch.cuda.mem_get_info()[0]
+T._call(F, ops, "glt_adamw_graft_step_noalloc", st, 1, 1.0, ())
+torch.cuda.synchronize()
+free1 = torch.cuda.mem_get_info()[0]
+print("free", free0, free1, flush=True)
+sys.exit(0 if free0 == free1 else 3)
+"""
+
+
+def test_noalloc_first_call_allocates_nothing(dev):
+    """In a fresh process whose state was made with the library (so its code
+    object is loaded), the first allocation-free call (which looks up the
+    scratch address) leaves the device's free memory unchanged."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FRESH, root], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stdout
