@@ -87,6 +87,9 @@ def main():
     ap.add_argument("--eval-only", action="store_true",
                     help="only the shadow-eval measurement (for profiling it alone)")
     ap.add_argument("--cpu-tokens", type=int, default=4096)
+    ap.add_argument("--vendor", action="store_true",
+                    help="only the step's GEMM shapes on torch's bf16 GEMMs (hipBLASLt) beside this library's "
+                         "kernels in the same run, outside the timed step")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (scale for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -176,6 +179,10 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    if args.vendor:
+        print(json.dumps({"vendor_gemm": bench_vendor(torch, F, step, args, x, dy, wg, wu, wd, masters, inter)}),
+              flush=True)
+        return
 
     # timed region: K steps between events on the launch stream
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -319,6 +326,73 @@ def main():
                     for k, v in sorted(kernels.items())},
     }
     print(json.dumps(out), flush=True)
+
+
+def bench_vendor(torch, F, step, args, x, dy, wg, wu, wd, masters, inter, reps=10):
+    """The step's GEMM shapes on torch's bf16 GEMMs (hipBLASLt on this image)
+    next to this library's kernels from the same run (launch timing of the
+    step's own launches). Operands: the step's inputs where they exist (x,
+    the weights with the graft rows appended, the saved inter, dy rounded to
+    bf16); the dX GEMM's [dgate | dup] operand is drawn ~N(0, 0.01). Each
+    entry states what each side writes: the library's gate/up and dInter
+    GEMMs carry their epilogues (SiLU*up with three outputs; the SiLU*up
+    derivative reading two saved arrays and writing two), torch's write one
+    plain output."""
+    F.call("glt_profile_enable", 1)
+    for i in range(args.steps):
+        step(1000 + i)
+    torch.cuda.synchronize()
+    prof = F.profile_collect()
+    F.call("glt_profile_enable", 0)
+    ours = {k: tot / cnt for k, (tot, cnt) in prof.items()}
+    bf = torch.bfloat16
+    gd = masters[:S * D].view(S, D).to(bf)
+    ud = masters[S * D:2 * S * D].view(S, D).to(bf)
+    dd = masters[2 * S * D:].view(S, D).to(bf)
+    w_gu = torch.cat([wg, gd, wu, ud], 0)                  # [2N, D]
+    w_down = torch.cat([wd, dd.t()], 1).contiguous()       # [D, N]
+    w_down_t = w_down.t().contiguous()                     # [N, D]
+    w_dx = torch.cat([wg, gd, wu, ud], 0)                  # [2N, D]: dX = [dg | du] . w_dx
+    dyb = dy.to(bf)
+    dgdu = torch.empty((M, 2 * N), dtype=bf, device=x.device).normal_(0.0, 0.01)
+    try:
+        torch.mm(dyb[:64], w_down[:, :64], out_dtype=torch.float32)
+        dx_f32 = True
+    except Exception:   # no mixed-output mm in this torch build
+        dx_f32 = False
+    cases = {
+        "gate_up": (lambda: torch.nn.functional.linear(x, w_gu), "[M, 2N] bf16 = %d B" % (M * 2 * N * 2),
+                    "inter, gate_pre, up_pre [M, N] bf16 = %d B (SiLU*up epilogue)" % (3 * M * N * 2)),
+        "down": (lambda: torch.nn.functional.linear(inter, w_down), "[M, D] bf16 = %d B" % (M * D * 2),
+                 "[M, D] bf16 = %d B" % (M * D * 2)),
+        "dinter": (lambda: torch.nn.functional.linear(dyb, w_down_t), "[M, N] bf16 = %d B" % (M * N * 2),
+                   "dgate, dup [M, N] bf16 = %d B, reading gate_pre, up_pre = %d B (SiLU*up derivative)"
+                   % (2 * M * N * 2, 2 * M * N * 2)),
+        "dx": ((lambda: torch.mm(dgdu, w_dx, out_dtype=torch.float32)) if dx_f32 else (lambda: torch.mm(dgdu, w_dx)),
+               "[M, D] %s = %d B" % (("f32", M * D * 4) if dx_f32 else ("bf16", M * D * 2)),
+               "[M, D] f32 = %d B" % (M * D * 4)),
+    }
+    out = {}
+    stream = torch.cuda.current_stream()
+    for k, (fn, tb, ob) in cases.items():
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / reps
+        o = ours.get(k)
+        out[k] = {"flop": GEMM_FLOP[k], "torch_ms": round(t, 4), "torch_tflops": round(GEMM_FLOP[k] / t / 1e9, 1),
+                  "torch_writes": tb, "ours_ms": round(o, 4) if o else None,
+                  "ours_tflops": round(GEMM_FLOP[k] / o / 1e9, 1) if o else None, "ours_writes": ob}
+        log(f"[bench] {k}: torch {t:.3f} ms, ours {o:.3f} ms")
+    out["note"] = ("torch times are back-to-back launches between events on the stream; ours are the step's "
+                   "launches timed by events bound to each dispatch")
+    return out
 
 
 def bench_rope(torch, F, sp, p, cold_ms):

@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   const int b = blockIdx.x;
   const int first = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
 
-  auto next_active = [&](const GProb& P, int n0, int s, int send) {
+  auto next_active = [&](const GProb& P, int n0, int s, int send) __attribute__((always_inline)) {
     ++s;
     while (s < send && !seg_hits(args.s[s], P, n0, BN)) ++s;
     return s;
@@ -228,7 +228,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   };
   // Moves q to the first active segment of tile q.t or of a later tile of
   // this workgroup (tiles without one have no K-steps); false past the end.
-  auto first_seg = [&](Pos& q) {
+  auto first_seg = [&](Pos& q) __attribute__((always_inline)) {
     for (; q.t < total; q.t += G) {
       int tm, tn;
       q.pi = locate_tile(args, q.t, tm, tn);
@@ -245,19 +245,30 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
     }
     return false;
   };
-  // One K-step on: 0 = same segment, 1 = a new segment, 2 = past the end.
-  auto step_pos = [&](Pos& q) {
-    if (q.t >= total) return 2;
-    q.k += kBK;
-    if (q.k < q.K) return 0;
+  // One K-step on, after the caller has added kBK to q.k and found q.k >=
+  // q.K: the next active segment of the tile, else the first of a later
+  // tile (1), or the end of the stream (2). The common step (same segment)
+  // stays in the K loop as one add and a branch not taken; this cold part
+  // runs once per segment. Past the end the stream's K is kNoEnd, so it is
+  // not entered again, and q.k restarts at 0 (the trailing loads' offsets
+  // are kOob, so the scalar offset only has to stay small).
+  constexpr int kNoEnd = 1 << 30;
+  auto step_cold = [&](Pos& q) __attribute__((always_inline)) {
     q.k = 0;
+    if (q.t >= total) {
+      q.K = kNoEnd;
+      return 2;
+    }
     q.s = next_active(args.p[q.pi], q.n0, q.s, q.send);
     if (q.s < q.send) {
       q.K = args.s[q.s].K;
       return 1;
     }
     q.t += G;
-    return first_seg(q) ? 1 : 2;
+    if (first_seg(q)) return 1;
+    q.k = 0;
+    q.K = kNoEnd;
+    return 2;
   };
 
   // ---- A side: 8 direct-to-LDS loads per wavefront per K-step; load i of
@@ -269,7 +280,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   Pos pa{first, 0, 0, 0, 0, 0, 0, 0};
   const void* pA = nullptr;
   uint32_t nA = 0, voA[8];
-  auto setup_a = [&]() {
+  auto setup_a = [&]() __attribute__((always_inline)) {
     const GSeg& S = args.s[pa.s];
     const GProb& P = args.p[pa.pi];
     pA = S.A;
@@ -282,14 +293,16 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
       voA[i] = m < P.M ? (uint32_t)(((int64_t)m * S.lda + S.a_col + kc * 8) * 2) : kOob;
     }
   };
-  auto end_a = [&]() {
+  auto end_a = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) voA[i] = kOob;
   };
-  auto adv_a = [&]() {
-    const int r = step_pos(pa);
-    if (r == 1) setup_a();
-    else if (r == 2) end_a();
+  auto adv_a = [&]() __attribute__((always_inline)) {
+    pa.k += kBK;
+    if (__builtin_expect(pa.k >= pa.K, 0)) {
+      if (step_cold(pa) == 1) setup_a();
+      else end_a();
+    }
   };
   typedef __attribute__((address_space(3))) void lds_void;
   auto load_a = [&](int stage, int i) {
@@ -304,7 +317,7 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
   Pos pb{first, 0, 0, 0, 0, 0, 0, 0};
   const void *pB0 = nullptr, *pB1 = nullptr;
   uint32_t nB0 = 0, nB1 = 0, voB[4];
-  auto setup_b = [&]() {
+  auto setup_b = [&]() __attribute__((always_inline)) {
     const GSeg& S = args.s[pb.s];
     const GProb& P = args.p[pb.pi];
     pB0 = S.B0;
@@ -325,14 +338,16 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
 #pragma unroll
     for (int j = 2; j < 4; ++j) voB[j] = DUAL ? voff(j, S.ldb1, S.b1_row0) : voff(j, S.ldb0, S.b0_row0);
   };
-  auto end_b = [&]() {
+  auto end_b = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) voB[j] = kOob;
   };
-  auto adv_b = [&]() {
-    const int r = step_pos(pb);
-    if (r == 1) setup_b();
-    else if (r == 2) end_b();
+  auto adv_b = [&]() __attribute__((always_inline)) {
+    pb.k += kBK;
+    if (__builtin_expect(pb.k >= pb.K, 0)) {
+      if (step_cold(pb) == 1) setup_b();
+      else end_b();
+    }
   };
   bf16x8 fb[4][4];  // [substep][fragment]
   auto load_b = [&](int s, int j) {
@@ -376,7 +391,10 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
 
   // Pipeline fill: A tiles of K-steps 0..2 into stages 0..2, loads 0-1 of
   // step 3 (the rest follow in step 0), B of step 0.
-  first_seg(pa);
+  if (!first_seg(pa)) {
+    pa.k = 0;
+    pa.K = kNoEnd;
+  }
   pb = pa;
   if (pa.t < total) {
     setup_a();
@@ -398,8 +416,11 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) load_b(s, j);
   adv_b();
-  // A of step 0: issued first, followed by 18 more A loads and 16 B loads
-  __builtin_amdgcn_s_waitcnt(vmcnt_enc(34));
+  // A of steps 0 and 1: the last load of step 1 is followed by 8 A loads of
+  // step 2, 2 of step 3 and the 16 B loads. With step 1 landed here, the
+  // first K-step needs no wait of its own (as the first step after an
+  // epilogue).
+  __builtin_amdgcn_s_waitcnt(vmcnt_enc(26));
   ring_barrier();
 #pragma unroll
   for (int i = 0; i < 4; ++i) read_a(0, 0, 0, i);
@@ -407,8 +428,8 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
 
   char* const ep = reinterpret_cast<char*>(smem) + (size_t)kAStages * kTileElems * 2 + wave * kEpWaveBytes;
   // A of the step after the current one is already known to have landed
-  // (waited for before the last epilogue)
-  bool prewaited = false;
+  // (waited for before the last epilogue, or in the pipeline fill)
+  bool prewaited = true;
   for (int ct = first; ct < total; ct += G) {
     int tm, tn;
     const int pi = locate_tile(args, ct, tm, tn);
@@ -450,15 +471,10 @@ __global__ void __launch_bounds__(256, 1) gemm_mfma_kernel(const GArgs args) {
       // has at least n loads issued after it. The last A load of step g+1
       // was issued at the end of phase 2 of step g-2; after it come 48
       // loads (phase 3 of step g-2, step g-1, phases 0-2 of step g: 6 per
-      // phase), or 44 in step 0 (the fill order). Stores in between only
-      // raise the count. Right after an epilogue that wait was already done
-      // before it, with no stores outstanding.
-      if (prewaited) {
-      } else if (g == 0) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_enc(44));
-      } else {
-        __builtin_amdgcn_s_waitcnt(vmcnt_enc(48));
-      }
+      // phase). Stores in between only raise the count. In the first step
+      // of the kernel and right after an epilogue that wait was already
+      // done, with no stores outstanding.
+      if (__builtin_expect(!prewaited, 1)) __builtin_amdgcn_s_waitcnt(vmcnt_enc(48));
       prewaited = false;
       ring_barrier();
       __builtin_amdgcn_sched_barrier(0);
