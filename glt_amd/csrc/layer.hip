@@ -401,7 +401,13 @@ __global__ void __launch_bounds__(256) eval_row_stats_kernel(const uint16_t* log
   const int64_t r = blockIdx.x;
   const uint16_t* x = logits + r * ld;
   double s = 0.0, s2 = 0.0;
-  float m = -3.402823466e38f, se = 0.f;  // a finite start keeps exp(-inf - m) at 0
+  // The running maximum starts finite and low (-2^126: times log2(e) it
+  // stays finite), so exp(-inf - m) is 0 and the first chunk's rescale of
+  // the zero sum needs no test. Each chunk rescales the sum to the new
+  // maximum (a factor of 1 when it did not grow), branch-free; exp(x - m)
+  // is exp2(x log2(e) - m log2(e)), one fma per logit.
+  constexpr float kLog2e = 1.4426950408889634f;
+  float m = -8.5070592e37f, se = 0.f;
   auto add8 = [&](const u32x4& q) {
     float f[8];
 #pragma unroll
@@ -412,13 +418,13 @@ __global__ void __launch_bounds__(256) eval_row_stats_kernel(const uint16_t* log
     float lm = f[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) lm = fmaxf(lm, f[e]);
-    if (lm > m) {
-      se *= __expf(m - lm);
-      m = lm;
-    }
+    const float mn = fmaxf(m, lm);
+    const float mn2 = mn * kLog2e;
+    se *= __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -mn2));
+    m = mn;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      se += __expf(f[e] - m);
+      se += __builtin_amdgcn_exp2f(fmaf(f[e], kLog2e, -mn2));
       // squared in f64 like the reference (static_cast<double>(f) * f): the
       // f32 square of a large or tiny logit overflows or underflows; the
       // product of two f32 values is exact in f64, so one fma is the

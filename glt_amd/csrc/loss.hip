@@ -119,6 +119,7 @@ __device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
   const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(uint32_t, v);
 }
+template <bool SCALED>
 __device__ __forceinline__ u32x4 grad_chunk(u32x4 c, float m2, float inv_s, float inv_n, float scale) {
   const uint32_t ws[4] = {c.x, c.y, c.z, c.w};
   uint32_t out[4];
@@ -128,7 +129,7 @@ __device__ __forceinline__ u32x4 grad_chunk(u32x4 c, float m2, float inv_s, floa
     const float p1 = __builtin_amdgcn_exp2f(fmaf(bf_hi(ws[q]), kLog2e, -m2)) * inv_s;
     const uint32_t pb = cvt2(p0, p1);
     uint32_t gb = cvt2(bf_lo(pb) * inv_n, bf_hi(pb) * inv_n);
-    if (scale != 1.0f) gb = cvt2(bf_lo(gb) * scale, bf_hi(gb) * scale);
+    if constexpr (SCALED) gb = cvt2(bf_lo(gb) * scale, bf_hi(gb) * scale);
     out[q] = gb;
   }
   return u32x4{out[0], out[1], out[2], out[3]};
@@ -157,7 +158,6 @@ __device__ __forceinline__ void store_chunk(uint16_t* g, u32x4 v, int e, int V, 
 template <bool RESIDENT>
 __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
   __shared__ float red[kCeWaves];
-  __shared__ float x_label;
   const int row = blockIdx.x;
   const int b = row / a.T, t = row - b * a.T;
   const int tid = threadIdx.x;
@@ -173,17 +173,21 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
   const bool vec = (a.ld % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.logits) & 15) == 0);
   const int label = a.ids[(int64_t)b * a.T + t + 1];
   const bool valid_label = label >= 0 && label < a.V;
+  // the label's logit: one load per row, issued before the row's loads
+  const float x_label = valid_label ? bf16_to_f32(x[label]) : 0.f;
   const float mask = (a.ood && a.ood[(int64_t)b * a.T + t + 1] != 0) ? 0.f : 1.f;
   const int nchunks = (a.V + 7) / 8;
 
   u32x4 c[RESIDENT ? kCeChunks : 1];
   // pass 1: per-thread running max and sum of exp(x - max) over its chunks
-  // (each chunk's values unpacked once), then combined over the block
-  float mt = -INFINITY, st = 0.f;
-  // the label's logit is taken from the chunk that holds it (no dependent
-  // global load on the row's critical path)
-  const int lab_chunk = valid_label ? label >> 3 : -1;
-  auto fold = [&](u32x4 v, int ci) {
+  // (each chunk's values unpacked once), then combined over the block. The
+  // running max starts finite and low (-2^126, not -inf): a first chunk
+  // then rescales a zero sum by exp2 of a large negative number (0), and
+  // -inf logits (the generic path's padding) add exp2(-inf) = 0, with no
+  // per-chunk test for either.
+  constexpr float kLowMax = -8.5070592e37f;  // -2^126: times log2(e) stays finite
+  float mt = kLowMax, st = 0.f;
+  auto fold = [&](u32x4 v) {
     const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
     float xs[8];
 #pragma unroll
@@ -191,22 +195,15 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
       xs[2 * q] = bf_lo(ws[q]);
       xs[2 * q + 1] = bf_hi(ws[q]);
     }
-    if (ci == lab_chunk) {
-      float xl = xs[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) xl = (label & 7) == e ? xs[e] : xl;
-      x_label = xl;
-    }
     float mc = xs[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) mc = fmaxf(mc, xs[e]);
     const float mn = fmaxf(mt, mc);
-    if (mn == -INFINITY) return;  // nothing but padding so far
     const float mn2 = mn * kLog2e;
     float sc = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) sc += __builtin_amdgcn_exp2f(fmaf(xs[e], kLog2e, -mn2));
-    st = (mt == -INFINITY ? 0.f : st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -mn2))) + sc;
+    st = st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -mn2)) + sc;
     mt = mn;
   };
   // resident rows (V % 8 == 0, 16-byte aligned rows) use buffer accesses:
@@ -221,17 +218,17 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
 #pragma unroll
     for (int k = 0; k < kCeChunks; ++k) {
       // chunks past the row (zeros from beyond the descriptor's extent) are skipped
-      if (tid + k * kCeThreads < nchunks) fold(c[k], tid + k * kCeThreads);
+      if (tid + k * kCeThreads < nchunks) fold(c[k]);
       // the gradient pass unpacks the chunk again rather than keeping
       // these values alive (128 more registers)
       asm volatile("" : "+v"(c[k]));
     }
   } else {
-    for (int ci = tid; ci < nchunks; ci += kCeThreads) fold(load_chunk(x, ci * 8, a.V, vec), ci);
+    for (int ci = tid; ci < nchunks; ci += kCeThreads) fold(load_chunk(x, ci * 8, a.V, vec));
   }
   const float m = block_max(mt, red);
   const float m2 = m * kLog2e;
-  const float s = block_sum(mt == -INFINITY ? 0.f : st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m2)), red);
+  const float s = block_sum(st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m2)), red);
   const float inv_s = 1.0f / s;
   const float n = a.stats[3];
   const float inv_n = 1.0f / n;
@@ -240,7 +237,7 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
   if (tid == 0) {
     float ce_v = NAN, xl = NAN, pl = NAN;
     if (valid_label) {
-      xl = x_label;  // written before the block reductions' barriers
+      xl = x_label;
       const float logsum = logf(s);
       ce_v = -rbf((xl - m) - logsum);
       pl = rbf(__builtin_amdgcn_exp2f(fmaf(xl, kLog2e, -m2)) * inv_s);
@@ -252,8 +249,10 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
     a.partial[2 * R + r] = pl * mask;
   }
   if (!g) return;
-  // the label element in full: bf16(p) - 1, * mask, * (1/n), * scale, each
-  // rounded; an excluded row is +0 elsewhere (p >= 0) and skips the exps
+  // pass 3: gradient. An excluded row (mask 0, uniform over the block) is
+  // +0 everywhere but at the label (p >= 0, times 0) and skips the exps.
+  // The label element in full: bf16(p) - 1, * mask, * (1/n), * scale, each
+  // rounded, patched into its chunk by the thread that holds the chunk.
   uint32_t gl = 0;
   if (valid_label) {
     float v = rbf(__builtin_amdgcn_exp2f(fmaf(x_label, kLog2e, -m2)) * inv_s);
@@ -263,25 +262,40 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
     gl = f32_to_bf16(v * a.scale);
   }
   const bool masked = mask == 0.f;
-  auto row_chunk = [&](u32x4 v, int ci) {
-    u32x4 o = masked ? u32x4{0u, 0u, 0u, 0u} : grad_chunk(v, m2, inv_s, inv_n, a.scale);
-    if (ci == lab_chunk) o = patch_chunk(o, label & 7, gl);
-    return o;
-  };
-  // pass 3: gradient
+  const int lab_chunk = valid_label ? label >> 3 : -1;
   if constexpr (RESIDENT) {
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (uint32_t)a.V * 2);
+    // which of the resident chunks holds the label is the same for every
+    // thread, so only that one pays for the patch
+    const int lab_k = valid_label ? lab_chunk / kCeThreads : -1;
+    const bool lab_mine = valid_label && lab_chunk % kCeThreads == tid;
+    // one loop per case (the case is the same for the whole row)
+    auto stores = [&](auto chunk_of) {
 #pragma unroll
-    for (int k = 0; k < kCeChunks; ++k) {
-      // stores past the row fall outside the descriptor and are dropped
-      const int ci = tid + k * kCeThreads;
-      __builtin_amdgcn_raw_buffer_store_b128(row_chunk(c[k], ci), rg, vo, k * a.chunk_stride, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+      for (int k = 0; k < kCeChunks; ++k) {
+        u32x4 o = chunk_of(c[k]);
+        if (k == lab_k && lab_mine) o = patch_chunk(o, label & 7, gl);
+        // stores past the row fall outside the descriptor and are dropped.
+        // The chunk offset rides in the per-lane offset, not the scalar one:
+        // a 16-byte store needs wait states before its data registers are
+        // rewritten, and the compiler leaves them out for buffer stores
+        // with a register scalar offset (which on gfx950 then store the
+        // next chunk's values).
+        __builtin_amdgcn_raw_buffer_store_b128(o, rg, vo + k * a.chunk_stride, 0, 0);
+      }
+    };
+    if (masked) stores([](u32x4) { return u32x4{0u, 0u, 0u, 0u}; });
+    else if (a.scale == 1.0f) stores([&](u32x4 v) { return grad_chunk<false>(v, m2, inv_s, inv_n, a.scale); });
+    else stores([&](u32x4 v) { return grad_chunk<true>(v, m2, inv_s, inv_n, a.scale); });
   } else {
-    for (int ci = tid; ci < nchunks; ci += kCeThreads)
-      store_chunk(g, row_chunk(masked ? u32x4{0u, 0u, 0u, 0u} : load_chunk(x, ci * 8, a.V, vec), ci), ci * 8, a.V,
-                  gvec);
+    for (int ci = tid; ci < nchunks; ci += kCeThreads) {
+      const u32x4 xc = load_chunk(x, ci * 8, a.V, vec);
+      u32x4 o = masked ? u32x4{0u, 0u, 0u, 0u}
+                       : a.scale == 1.0f ? grad_chunk<false>(xc, m2, inv_s, inv_n, a.scale)
+                                         : grad_chunk<true>(xc, m2, inv_s, inv_n, a.scale);
+      if (ci == lab_chunk) o = patch_chunk(o, label & 7, gl);
+      store_chunk(g, o, ci * 8, a.V, gvec);
+    }
   }
 }
 
