@@ -22,7 +22,9 @@
 // written once; larger vocabularies re-read the row for the gradient.
 // exp is exp2 of a pre-scaled argument (a few ulp in f32 before the bf16
 // rounding); the row sum's order differs from ATen's block reduction.
+#include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -35,6 +37,11 @@ constexpr int kCeWaves = kCeThreads / 64;
 constexpr int kCeChunks = 16;                                   // 16-byte chunks per thread (resident)
 constexpr int kCeResidentV = kCeThreads * kCeChunks * 8;        // 131072
 constexpr float kLog2e = 1.4426950408889634f;
+// Cache policies of the resident rows' loads, gradient stores and zero rows:
+// the nontemporal bit on the stores (a gradient is written once) measured
+// 4.5 % faster at 4 x 4096 x 128256 with every third token excluded, on
+// the loads 4 % slower.
+constexpr int kCeAuxLd = 0, kCeAuxSt = 2, kCeAuxZero = 2;
 constexpr uint16_t kBf16NegInf = 0xFF80u;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -112,21 +119,24 @@ struct CeArgs {
 // Gradient of one chunk of an unmasked row (8 elements), packed bf16:
 // bf16(bf16(bf16(p) * (1/n)) * scale) with the hardware RNE conversion
 // (v_cvt_pk_bf16_f32, equal to the bias-and-shift rounding for finite
-// values); the label element is patched in afterwards. mask = 1 makes
-// the reference's bf16(g * mask) exact, and scale == 1 its last step.
+// values); the label element is patched in afterwards. mask = 1 makes the
+// reference's bf16(g * mask) exact, and scale == 1 its last step. p =
+// exp(x - m) / s is formed as exp2(x log2(e) - c) with c = m log2(e) +
+// log2(s), one fma per element (c is rounded once per row: a few ulp of p,
+// the same for the whole row).
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
   const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(uint32_t, v);
 }
 template <bool SCALED>
-__device__ __forceinline__ u32x4 grad_chunk(u32x4 c, float m2, float inv_s, float inv_n, float scale) {
+__device__ __forceinline__ u32x4 grad_chunk(u32x4 c, float cexp, float inv_n, float scale) {
   const uint32_t ws[4] = {c.x, c.y, c.z, c.w};
   uint32_t out[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const float p0 = __builtin_amdgcn_exp2f(fmaf(bf_lo(ws[q]), kLog2e, -m2)) * inv_s;
-    const float p1 = __builtin_amdgcn_exp2f(fmaf(bf_hi(ws[q]), kLog2e, -m2)) * inv_s;
+    const float p0 = __builtin_amdgcn_exp2f(fmaf(bf_lo(ws[q]), kLog2e, -cexp));
+    const float p1 = __builtin_amdgcn_exp2f(fmaf(bf_hi(ws[q]), kLog2e, -cexp));
     const uint32_t pb = cvt2(p0, p1);
     uint32_t gb = cvt2(bf_lo(pb) * inv_n, bf_hi(pb) * inv_n);
     if constexpr (SCALED) gb = cvt2(bf_lo(gb) * scale, bf_hi(gb) * scale);
@@ -155,7 +165,73 @@ __device__ __forceinline__ void store_chunk(uint16_t* g, u32x4 v, int e, int V, 
   }
 }
 
-template <bool RESIDENT>
+// Running max and sum of exp(x - max) over a thread's chunks, each chunk's
+// values unpacked once. The running max starts finite and low (kCeLowMax =
+// -2^126, not -inf): a first chunk then rescales a zero sum by exp2 of a
+// large negative number (0), and -inf logits (the generic path's padding)
+// add exp2(-inf) = 0, with no per-chunk test for either.
+constexpr float kCeLowMax = -8.5070592e37f;  // -2^126: times log2(e) stays finite
+__device__ __forceinline__ void ce_fold(float& mt, float& st, u32x4 v) {
+  const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+  float xs[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    xs[2 * q] = bf_lo(ws[q]);
+    xs[2 * q + 1] = bf_hi(ws[q]);
+  }
+  float mc = xs[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mc = fmaxf(mc, xs[e]);
+  const float mn = fmaxf(mt, mc);
+  const float mn2 = mn * kLog2e;
+  float sc = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sc += __builtin_amdgcn_exp2f(fmaf(xs[e], kLog2e, -mn2));
+  st = st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -mn2)) + sc;
+  mt = mn;
+}
+
+// One scored row's reference terms once its max m (m2 = m log2 e) and sum s
+// are known: thread 0 writes ce, and the ce / target-logit / target-
+// probability partials; every thread gets the label's gradient element in
+// full: bf16(p) - 1, * mask, * (1/n), * scale, each rounded.
+struct CeRowTerms {
+  float m2, inv_s, inv_n, cexp;  // cexp = m log2(e) + log2(s)
+  uint32_t gl;
+};
+__device__ __forceinline__ CeRowTerms ce_row_terms(const CeArgs& a, int r, bool valid_label, float x_label,
+                                                    float mask, float m, float s) {
+  CeRowTerms o;
+  o.m2 = m * kLog2e;
+  o.inv_s = 1.0f / s;
+  o.inv_n = 1.0f / a.stats[3];
+  o.cexp = o.m2 + log2f(s);
+  if (threadIdx.x == 0) {
+    float ce_v = NAN, xl = NAN, pl = NAN;
+    if (valid_label) {
+      xl = x_label;
+      ce_v = -rbf((xl - m) - logf(s));
+      pl = rbf(__builtin_amdgcn_exp2f(fmaf(xl, kLog2e, -o.m2)) * o.inv_s);
+    }
+    if (a.ce) a.ce[r] = ce_v;
+    const int R = a.B * (a.T - 1);
+    a.partial[r] = ce_v * mask;
+    a.partial[R + r] = xl * mask;
+    a.partial[2 * R + r] = pl * mask;
+  }
+  o.gl = 0;
+  if (valid_label) {
+    float v = rbf(__builtin_amdgcn_exp2f(fmaf(x_label, kLog2e, -o.m2)) * o.inv_s);
+    v = rbf(v - 1.0f);
+    v = rbf(v * mask);
+    v = rbf(v * o.inv_n);
+    o.gl = f32_to_bf16(v * a.scale);
+  }
+  return o;
+}
+
+// Generic rows (V past the resident size, or unaligned rows): one workgroup
+// per row, the row read twice (max and sum, then the gradient).
 __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
   __shared__ float red[kCeWaves];
   const int row = blockIdx.x;
@@ -173,130 +249,106 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
   const bool vec = (a.ld % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.logits) & 15) == 0);
   const int label = a.ids[(int64_t)b * a.T + t + 1];
   const bool valid_label = label >= 0 && label < a.V;
-  // the label's logit: one load per row, issued before the row's loads
   const float x_label = valid_label ? bf16_to_f32(x[label]) : 0.f;
   const float mask = (a.ood && a.ood[(int64_t)b * a.T + t + 1] != 0) ? 0.f : 1.f;
   const int nchunks = (a.V + 7) / 8;
-
-  u32x4 c[RESIDENT ? kCeChunks : 1];
-  // pass 1: per-thread running max and sum of exp(x - max) over its chunks
-  // (each chunk's values unpacked once), then combined over the block. The
-  // running max starts finite and low (-2^126, not -inf): a first chunk
-  // then rescales a zero sum by exp2 of a large negative number (0), and
-  // -inf logits (the generic path's padding) add exp2(-inf) = 0, with no
-  // per-chunk test for either.
-  constexpr float kLowMax = -8.5070592e37f;  // -2^126: times log2(e) stays finite
-  float mt = kLowMax, st = 0.f;
-  auto fold = [&](u32x4 v) {
-    const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
-    float xs[8];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      xs[2 * q] = bf_lo(ws[q]);
-      xs[2 * q + 1] = bf_hi(ws[q]);
-    }
-    float mc = xs[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) mc = fmaxf(mc, xs[e]);
-    const float mn = fmaxf(mt, mc);
-    const float mn2 = mn * kLog2e;
-    float sc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sc += __builtin_amdgcn_exp2f(fmaf(xs[e], kLog2e, -mn2));
-    st = st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -mn2)) + sc;
-    mt = mn;
-  };
-  // resident rows (V % 8 == 0, 16-byte aligned rows) use buffer accesses:
-  // one per-lane byte offset, the chunk index in the scalar offset (no
-  // per-chunk address registers)
-  const uint32_t vo = (uint32_t)tid * 16;
-  if constexpr (RESIDENT) {
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)a.V * 2);
-#pragma unroll
-    for (int k = 0; k < kCeChunks; ++k)
-      c[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, k * a.chunk_stride, 0));
-#pragma unroll
-    for (int k = 0; k < kCeChunks; ++k) {
-      // chunks past the row (zeros from beyond the descriptor's extent) are skipped
-      if (tid + k * kCeThreads < nchunks) fold(c[k]);
-      // the gradient pass unpacks the chunk again rather than keeping
-      // these values alive (128 more registers)
-      asm volatile("" : "+v"(c[k]));
-    }
-  } else {
-    for (int ci = tid; ci < nchunks; ci += kCeThreads) fold(load_chunk(x, ci * 8, a.V, vec));
-  }
+  float mt = kCeLowMax, st = 0.f;
+  for (int ci = tid; ci < nchunks; ci += kCeThreads) ce_fold(mt, st, load_chunk(x, ci * 8, a.V, vec));
   const float m = block_max(mt, red);
-  const float m2 = m * kLog2e;
-  const float s = block_sum(st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m2)), red);
-  const float inv_s = 1.0f / s;
-  const float n = a.stats[3];
-  const float inv_n = 1.0f / n;
-
-  // per-row terms (thread 0): ce, target logit, target probability
-  if (tid == 0) {
-    float ce_v = NAN, xl = NAN, pl = NAN;
-    if (valid_label) {
-      xl = x_label;
-      const float logsum = logf(s);
-      ce_v = -rbf((xl - m) - logsum);
-      pl = rbf(__builtin_amdgcn_exp2f(fmaf(xl, kLog2e, -m2)) * inv_s);
-    }
-    if (a.ce) a.ce[r] = ce_v;
-    const int R = a.B * (a.T - 1);
-    a.partial[r] = ce_v * mask;
-    a.partial[R + r] = xl * mask;
-    a.partial[2 * R + r] = pl * mask;
-  }
+  const float s = block_sum(st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m * kLog2e)), red);
+  const CeRowTerms w = ce_row_terms(a, r, valid_label, x_label, mask, m, s);
   if (!g) return;
-  // pass 3: gradient. An excluded row (mask 0, uniform over the block) is
-  // +0 everywhere but at the label (p >= 0, times 0) and skips the exps.
-  // The label element in full: bf16(p) - 1, * mask, * (1/n), * scale, each
-  // rounded, patched into its chunk by the thread that holds the chunk.
-  uint32_t gl = 0;
-  if (valid_label) {
-    float v = rbf(__builtin_amdgcn_exp2f(fmaf(x_label, kLog2e, -m2)) * inv_s);
-    v = rbf(v - 1.0f);
-    v = rbf(v * mask);
-    v = rbf(v * inv_n);
-    gl = f32_to_bf16(v * a.scale);
-  }
+  // an excluded row (mask 0) is +0 everywhere but at the label
   const bool masked = mask == 0.f;
   const int lab_chunk = valid_label ? label >> 3 : -1;
-  if constexpr (RESIDENT) {
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (uint32_t)a.V * 2);
-    // which of the resident chunks holds the label is the same for every
-    // thread, so only that one pays for the patch
-    const int lab_k = valid_label ? lab_chunk / kCeThreads : -1;
-    const bool lab_mine = valid_label && lab_chunk % kCeThreads == tid;
-    // one loop per case (the case is the same for the whole row)
-    auto stores = [&](auto chunk_of) {
-#pragma unroll
-      for (int k = 0; k < kCeChunks; ++k) {
-        u32x4 o = chunk_of(c[k]);
-        if (k == lab_k && lab_mine) o = patch_chunk(o, label & 7, gl);
-        // stores past the row fall outside the descriptor and are dropped.
-        // The chunk offset rides in the per-lane offset, not the scalar one:
-        // a 16-byte store needs wait states before its data registers are
-        // rewritten, and the compiler leaves them out for buffer stores
-        // with a register scalar offset (which on gfx950 then store the
-        // next chunk's values).
-        __builtin_amdgcn_raw_buffer_store_b128(o, rg, vo + k * a.chunk_stride, 0, 0);
-      }
-    };
-    if (masked) stores([](u32x4) { return u32x4{0u, 0u, 0u, 0u}; });
-    else if (a.scale == 1.0f) stores([&](u32x4 v) { return grad_chunk<false>(v, m2, inv_s, inv_n, a.scale); });
-    else stores([&](u32x4 v) { return grad_chunk<true>(v, m2, inv_s, inv_n, a.scale); });
-  } else {
-    for (int ci = tid; ci < nchunks; ci += kCeThreads) {
-      const u32x4 xc = load_chunk(x, ci * 8, a.V, vec);
-      u32x4 o = masked ? u32x4{0u, 0u, 0u, 0u}
-                       : a.scale == 1.0f ? grad_chunk<false>(xc, m2, inv_s, inv_n, a.scale)
-                                         : grad_chunk<true>(xc, m2, inv_s, inv_n, a.scale);
-      if (ci == lab_chunk) o = patch_chunk(o, label & 7, gl);
-      store_chunk(g, o, ci * 8, a.V, gvec);
-    }
+  for (int ci = tid; ci < nchunks; ci += kCeThreads) {
+    const u32x4 xc = load_chunk(x, ci * 8, a.V, vec);
+    u32x4 o = masked ? u32x4{0u, 0u, 0u, 0u}
+                     : a.scale == 1.0f ? grad_chunk<false>(xc, w.cexp, w.inv_n, a.scale)
+                                       : grad_chunk<true>(xc, w.cexp, w.inv_n, a.scale);
+    if (ci == lab_chunk) o = patch_chunk(o, label & 7, w.gl);
+    store_chunk(g, o, ci * 8, a.V, gvec);
   }
+}
+
+// Resident rows (V <= kCeResidentV, V % 8 == 0, 16-byte aligned rows): one
+// workgroup per row, the row in registers (chunk k of thread tid is chunk
+// tid + 1024 k of the row, 16 per thread), so the logits are read once and
+// the gradient written once. Buffer accesses: one per-lane byte offset, the
+// chunk index in the scalar offset of the loads (no per-chunk address
+// registers). LD and ST are the cache policies of the row's loads and the
+// gradient's stores, Z that of the stores of a zero row (a row without a
+// next token, or an excluded one: its gradient is 0 but at the label).
+template <int LD, int ST, int Z>
+__global__ void __launch_bounds__(kCeThreads) masked_ce_row_kernel(const CeArgs a) {
+  __shared__ float red[kCeWaves];
+  const int row = blockIdx.x;
+  const int b = row / a.T, t = row - b * a.T;
+  const int tid = threadIdx.x;
+  const uint32_t vo = (uint32_t)tid * 16;
+  uint16_t* g = a.grad ? a.grad + (int64_t)row * a.ld_grad : nullptr;
+  if (t == a.T - 1) {  // no next token: zero gradient row
+    if (g) {
+      const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (uint32_t)a.V * 2);
+#pragma unroll
+      for (int k = 0; k < kCeChunks; ++k)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rg, vo + k * a.chunk_stride, 0, Z);
+    }
+    return;
+  }
+  const uint16_t* x = a.logits + (int64_t)row * a.ld;
+  const int label = a.ids[(int64_t)b * a.T + t + 1];
+  const bool valid_label = label >= 0 && label < a.V;
+  // the label's logit: one load per row, issued before the row's loads
+  const float x_label = valid_label ? bf16_to_f32(x[label]) : 0.f;
+  const float mask = (a.ood && a.ood[(int64_t)b * a.T + t + 1] != 0) ? 0.f : 1.f;
+  const int nchunks = a.V >> 3;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)a.V * 2);
+  u32x4 c[kCeChunks];
+#pragma unroll
+  for (int k = 0; k < kCeChunks; ++k)
+    c[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, k * a.chunk_stride, LD));
+  float mt = kCeLowMax, st = 0.f;
+#pragma unroll
+  for (int k = 0; k < kCeChunks; ++k) {
+    // chunks past the row (zeros from beyond the descriptor's extent) are skipped
+    if (tid + k * kCeThreads < nchunks) ce_fold(mt, st, c[k]);
+    // the gradient pass unpacks the chunk again rather than keeping
+    // these values alive (128 more registers)
+    asm volatile("" : "+v"(c[k]));
+  }
+  const float m = block_max(mt, red);
+  const float s = block_sum(st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m * kLog2e)), red);
+  const CeRowTerms w = ce_row_terms(a, b * (a.T - 1) + t, valid_label, x_label, mask, m, s);
+  if (!g) return;
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (uint32_t)a.V * 2);
+  // which of the resident chunks holds the label is the same for every
+  // thread, so only that one pays for the patch
+  const int lab_chunk = valid_label ? label >> 3 : -1;
+  const int lab_k = valid_label ? lab_chunk / kCeThreads : -1;
+  const bool lab_mine = valid_label && lab_chunk % kCeThreads == tid;
+  // one loop per case (the case is the same for the whole row); an
+  // excluded row (mask 0) is +0 everywhere but at the label
+  auto stores = [&](auto chunk_of, auto policy) {
+#pragma unroll
+    for (int k = 0; k < kCeChunks; ++k) {
+      u32x4 o = chunk_of(c[k]);
+      if (k == lab_k && lab_mine) o = patch_chunk(o, label & 7, w.gl);
+      // stores past the row fall outside the descriptor and are dropped.
+      // The chunk offset rides in the per-lane offset, not the scalar one:
+      // a 16-byte store needs wait states before its data registers are
+      // rewritten, and the compiler leaves them out for buffer stores with
+      // a register scalar offset (which on gfx950 then store the next
+      // chunk's values).
+      __builtin_amdgcn_raw_buffer_store_b128(o, rg, vo + k * a.chunk_stride, 0, decltype(policy)::value);
+    }
+  };
+  using zero_policy = std::integral_constant<int, Z>;
+  using grad_policy = std::integral_constant<int, ST>;
+  if (mask == 0.f) stores([](u32x4) { return u32x4{0u, 0u, 0u, 0u}; }, zero_policy{});
+  else if (a.scale == 1.0f)
+    stores([&](u32x4 v) { return grad_chunk<false>(v, w.cexp, w.inv_n, a.scale); }, grad_policy{});
+  else stores([&](u32x4 v) { return grad_chunk<true>(v, w.cexp, w.inv_n, a.scale); }, grad_policy{});
 }
 
 // n = max(sum over scored rows of (1 - ood[b, t+1]), 1) into stats[3].
@@ -449,13 +501,13 @@ glt_status glt_masked_ce(const uint16_t* logits, int64_t ld, const int32_t* ids,
   if ((int64_t)B * T > 0) {
     CeArgs a{logits, ld,     ids, ood,   B, T, V, scale, grad, ld_grad, ce_per_token, static_cast<float*>(workspace),
              stats,  kCeThreads * 16};
-    const dim3 grid((unsigned)((int64_t)B * T));
+    const int64_t rows = (int64_t)B * T;
     const bool aligned = V % 8 == 0 && ld % 8 == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0 &&
                          (!grad || (ld_grad % 8 == 0 && (reinterpret_cast<uintptr_t>(grad) & 15) == 0));
     if (V <= kCeResidentV && aligned) {
-      GLT_LAUNCH("masked_ce", masked_ce_kernel<true>, grid, dim3(kCeThreads), 0, st, a);
+      GLT_LAUNCH("masked_ce", (masked_ce_row_kernel<kCeAuxLd, kCeAuxSt, kCeAuxZero>), dim3((unsigned)rows), dim3(kCeThreads), 0, st, a);
     } else {
-      GLT_LAUNCH("masked_ce", masked_ce_kernel<false>, grid, dim3(kCeThreads), 0, st, a);
+      GLT_LAUNCH("masked_ce", masked_ce_kernel, dim3((unsigned)rows), dim3(kCeThreads), 0, st, a);
     }
     GLT_LAUNCH_CHECK("masked_ce");
   }
