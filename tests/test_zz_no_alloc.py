@@ -135,6 +135,10 @@ from glt_amd import _ffi as F
 from glt_amd import ops
 import test_zz_no_alloc as T
 st = T._state(torch, ops, [(128, 256), (64, 96)], 70)
+# the workspace form launches kernels of the same source file, which loads
+# its code object (and with it the scratch array) onto the device
+ws = torch.empty(F.load().glt_adamw_workspace_size(0), dtype=torch.uint8, device="cuda")
+T._call(F, ops, "glt_adamw_graft_step", T._clone(torch, ops, st), 1, 1.0, (ctypes.c_void_p(ws.data_ptr()), ws.numel()))
 torch.cuda.synchronize()
 free0 = torch.cuda.mem_get_info()[0]
 T._call(F, ops, "glt_adamw_graft_step_noalloc", st, 1, 1.0, ())
@@ -146,9 +150,11 @@ sys.exit(0 if free0 == free1 else 3)
 
 
 def test_noalloc_first_call_allocates_nothing(dev):
-    """In a fresh process whose state was made with the library (so its code
-    object is loaded), the first allocation-free call (which looks up the
-    scratch address) leaves the device's free memory unchanged."""
+    """In a fresh process, after the workspace form has run (loading the code
+    object that holds the scratch array: 2 MiB of device memory, taken at the
+    first launch from that source file whichever entry point makes it), the
+    first allocation-free call (which looks up the scratch address) leaves
+    the device's free memory unchanged."""
     import os
     import subprocess
     import sys
