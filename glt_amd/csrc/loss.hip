@@ -83,6 +83,26 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   __syncthreads();
   return r;
 }
+// The same reductions for a workgroup that uses each red array once: no
+// barrier after the reads (nothing writes the array again).
+__device__ __forceinline__ float block_max_once(float v, float* red) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kCeWaves; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+__device__ __forceinline__ float block_sum_once(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < kCeWaves; ++i) r += red[i];
+  return r;
+}
 
 // 8 consecutive bf16 of a row starting at element e (e % 8 == 0); lanes of
 // the chunk past V read as -inf, which adds nothing to max or sum.
@@ -200,11 +220,11 @@ struct CeRowTerms {
   uint32_t gl;
 };
 __device__ __forceinline__ CeRowTerms ce_row_terms(const CeArgs& a, int r, bool valid_label, float x_label,
-                                                    float mask, float m, float s) {
+                                                    float mask, float m, float s, float n) {
   CeRowTerms o;
   o.m2 = m * kLog2e;
   o.inv_s = 1.0f / s;
-  o.inv_n = 1.0f / a.stats[3];
+  o.inv_n = 1.0f / n;
   o.cexp = o.m2 + log2f(s);
   if (threadIdx.x == 0) {
     float ce_v = NAN, xl = NAN, pl = NAN;
@@ -256,7 +276,7 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
   for (int ci = tid; ci < nchunks; ci += kCeThreads) ce_fold(mt, st, load_chunk(x, ci * 8, a.V, vec));
   const float m = block_max(mt, red);
   const float s = block_sum(st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m * kLog2e)), red);
-  const CeRowTerms w = ce_row_terms(a, r, valid_label, x_label, mask, m, s);
+  const CeRowTerms w = ce_row_terms(a, r, valid_label, x_label, mask, m, s, a.stats[3]);
   if (!g) return;
   // an excluded row (mask 0) is +0 everywhere but at the label
   const bool masked = mask == 0.f;
@@ -281,7 +301,8 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_kernel(const CeArgs a) {
 // next token, or an excluded one: its gradient is 0 but at the label).
 template <int LD, int ST, int Z>
 __global__ void __launch_bounds__(kCeThreads) masked_ce_row_kernel(const CeArgs a) {
-  __shared__ float red[kCeWaves];
+  __shared__ float red_m[kCeWaves], red_s[kCeWaves];
+  __shared__ float xl_sh;
   const int row = blockIdx.x;
   const int b = row / a.T, t = row - b * a.T;
   const int tid = threadIdx.x;
@@ -296,18 +317,29 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_row_kernel(const CeArgs 
     }
     return;
   }
+  // The row's loads go first: nothing they address depends on the row's
+  // label, mask or token count, whose loads are issued behind them.
   const uint16_t* x = a.logits + (int64_t)row * a.ld;
-  const int label = a.ids[(int64_t)b * a.T + t + 1];
-  const bool valid_label = label >= 0 && label < a.V;
-  // the label's logit: one load per row, issued before the row's loads
-  const float x_label = valid_label ? bf16_to_f32(x[label]) : 0.f;
-  const float mask = (a.ood && a.ood[(int64_t)b * a.T + t + 1] != 0) ? 0.f : 1.f;
   const int nchunks = a.V >> 3;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)a.V * 2);
   u32x4 c[kCeChunks];
+  // issued in chunk order (the scheduler otherwise moves chunk 0, whose
+  // scalar offset is the constant 0, behind the others, and the first fold
+  // then waits for nearly the whole row)
 #pragma unroll
-  for (int k = 0; k < kCeChunks; ++k)
+  for (int k = 0; k < kCeChunks; ++k) {
     c[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, vo, k * a.chunk_stride, LD));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const int label = a.ids[(int64_t)b * a.T + t + 1];
+  const float mask = (a.ood && a.ood[(int64_t)b * a.T + t + 1] != 0) ? 0.f : 1.f;
+  const float n_scored = a.stats[3];
+  const bool valid_label = label >= 0 && label < a.V;
+  // which of the resident chunks holds the label is the same for every
+  // thread (lab_k); one thread holds it
+  const int lab_chunk = valid_label ? label >> 3 : -1;
+  const int lab_k = valid_label ? lab_chunk / kCeThreads : -1;
+  const bool lab_mine = valid_label && lab_chunk % kCeThreads == tid;
   float mt = kCeLowMax, st = 0.f;
 #pragma unroll
   for (int k = 0; k < kCeChunks; ++k) {
@@ -317,16 +349,26 @@ __global__ void __launch_bounds__(kCeThreads) masked_ce_row_kernel(const CeArgs 
     // these values alive (128 more registers)
     asm volatile("" : "+v"(c[k]));
   }
-  const float m = block_max(mt, red);
-  const float s = block_sum(st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m * kLog2e)), red);
-  const CeRowTerms w = ce_row_terms(a, b * (a.T - 1) + t, valid_label, x_label, mask, m, s);
+  // the label's logit comes from the resident chunk that holds it, through
+  // LDS (published by the max reduction's barrier)
+  if (lab_mine) {
+    u32x4 lc = c[0];
+#pragma unroll
+    for (int k = 1; k < kCeChunks; ++k)
+      if (k == lab_k) lc = c[k];
+    const uint32_t wsel[4] = {lc.x, lc.y, lc.z, lc.w};
+    uint32_t wl = wsel[0];
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (q == ((label & 7) >> 1)) wl = wsel[q];
+    xl_sh = (label & 1) ? bf_hi(wl) : bf_lo(wl);
+  }
+  const float m = block_max_once(mt, red_m);
+  const float x_label = valid_label ? xl_sh : 0.f;
+  const float s = block_sum_once(st * __builtin_amdgcn_exp2f(fmaf(mt, kLog2e, -m * kLog2e)), red_s);
+  const CeRowTerms w = ce_row_terms(a, b * (a.T - 1) + t, valid_label, x_label, mask, m, s, n_scored);
   if (!g) return;
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (uint32_t)a.V * 2);
-  // which of the resident chunks holds the label is the same for every
-  // thread, so only that one pays for the patch
-  const int lab_chunk = valid_label ? label >> 3 : -1;
-  const int lab_k = valid_label ? lab_chunk / kCeThreads : -1;
-  const bool lab_mine = valid_label && lab_chunk % kCeThreads == tid;
   // one loop per case (the case is the same for the whole row); an
   // excluded row (mask 0) is +0 everywhere but at the label
   auto stores = [&](auto chunk_of, auto policy) {
