@@ -119,7 +119,8 @@ SIGNATURES = {
     "glt_rmsnorm_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "glt_rmsnorm_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "glt_rope_fwd": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
-    "glt_attention_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
+    "glt_attention_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _vp]),
+    "glt_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
     "glt_grft_save": (_i32, [ctypes.c_char_p, ctypes.POINTER(GrftInfo), _vp, _i32, _vp]),
     "glt_grft_load": (_i32, [ctypes.c_char_p, ctypes.POINTER(GrftInfo), _vp, _i32, _vp]),
     "glt_grft_load_raw_f32": (_i32, [ctypes.c_char_p, ctypes.POINTER(GrftInfo), _vp, _i32, _vp]),

@@ -49,7 +49,7 @@ Prep prep_layout(const glt_layer_desc* d) {
 // workspace: xn, q, k, v, attention output, RMSNorm mean squares, and the
 // MLP's inter when the caller does not keep it
 struct Ws {
-  size_t xn, q, k, v, a, var_in, var_post, inter, total;
+  size_t xn, q, k, v, a, var_in, var_post, inter, vt, total;
 };
 Ws ws_layout(const glt_layer_desc* d) {
   const Dims m = dims(d);
@@ -63,7 +63,8 @@ Ws ws_layout(const glt_layer_desc* d) {
   w.var_in = up(w.a + m.M * m.nq * 2);
   w.var_post = up(w.var_in + m.M * 4);
   w.inter = up(w.var_post + m.M * 4);
-  w.total = up(w.inter + m.M * N * 2);
+  w.vt = up(w.inter + m.M * N * 2);
+  w.total = up(w.vt + glt_attention_workspace_size(d->B, d->T, d->n_kv_heads, d->head_dim));
   return w;
 }
 
@@ -199,7 +200,7 @@ glt_status glt_layer_fwd(const glt_layer_desc* d, const glt_layer_weights* w, vo
     if (s != GLT_OK) return s;
   }
   s = glt_attention_fwd(q, k, v, a, d->B, d->T, d->n_q_heads, d->n_kv_heads, d->head_dim,
-                        1.0f / std::sqrt((float)d->head_dim), 1, stream);
+                        1.0f / std::sqrt((float)d->head_dim), 1, ws + L.vt, L.total - L.vt, stream);
   if (s != GLT_OK) return s;
   const Proj o = {w->o_proj, pb + P.o / 2, m.D, x};
   if ((s = project(a, m.M, m.nq, &o, 1, EPI_RESID, "o_proj", st)) != GLT_OK) return s;

@@ -213,8 +213,10 @@ def attention(q, k, v, causal=True, scale=None):
     if scale is None:
         scale = hd ** -0.5
     out = torch.empty_like(q)
+    nb = F.load().glt_attention_workspace_size(B, T, Hkv, hd)
+    ws = torch.empty(nb, dtype=torch.uint8, device=q.device)
     F.call("glt_attention_fwd", _p(q), _p(k), _p(v), _p(out), B, T, Hq, Hkv, hd, scale, 1 if causal else 0,
-           _stream())
+           _p(ws), nb, _stream())
     return out
 
 

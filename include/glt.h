@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GLT_ABI_VERSION 3
+#define GLT_ABI_VERSION 4
 
 /* ------------------------------------------------------------------ status */
 typedef int32_t glt_status;
@@ -306,10 +306,14 @@ glt_status glt_rope_fwd(uint16_t* q, int32_t n_q_heads, uint16_t* k, int32_t n_k
  * is 1/sqrt(head_dim)); causal != 0 masks keys after the query's position.
  * Softmax in f32 (online, exp2), probabilities rounded to bf16 for the P.V
  * product, f32 accumulation, one rounding of the output. head_dim must be
- * 128; tensors 16-byte aligned. */
+ * 128; tensors 16-byte aligned. workspace (glt_attention_workspace_size
+ * bytes, 256-byte aligned) receives a transposed copy of v, [B, n_kv_heads,
+ * head_dim, T rounded up to 64], rewritten by every call. */
+size_t glt_attention_workspace_size(int32_t B, int32_t T, int32_t n_kv_heads, int32_t head_dim);
 glt_status glt_attention_fwd(const void* q, const void* k, const void* v, void* out,
                              int32_t B, int32_t T, int32_t n_q_heads, int32_t n_kv_heads,
-                             int32_t head_dim, float scale, int32_t causal, void* stream);
+                             int32_t head_dim, float scale, int32_t causal, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------- decoder layer */
 /* One decoder layer forward with the grafted MLP (reference forward_layer,

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from glt_amd import _ffi
     lib = _ffi.load()
-    assert lib.glt_version() == 3
+    assert lib.glt_version() == 4
     assert isinstance(lib.glt_last_error_string(), bytes)
 
 
@@ -47,7 +47,10 @@ def test_host_validation_errors_without_gpu():
     bd = F.BakeDesc(0, 1, 0, 0, 7, 64, 64, 64, F.DTYPE_F32, 0, None, None)
     assert lib.glt_shadow_bake(ctypes.byref(bd), ctypes.byref(st), None, None, None, None, None, None, None) == 6
     # attention supports head_dim 128 only; refused before any GPU call
-    assert lib.glt_attention_fwd(1, 1, 1, 1, 1, 16, 4, 1, 64, 0.125, 1, None) == 9  # GLT_ERR_UNSUPPORTED
+    assert lib.glt_attention_fwd(1, 1, 1, 1, 1, 16, 4, 1, 64, 0.125, 1, None, 0, None) == 9  # GLT_ERR_UNSUPPORTED
+    # the transposed-V workspace: B x Hkv x 128 x (T rounded up to 64) bf16; refused when short
+    assert lib.glt_attention_workspace_size(2, 100, 4, 128) == 2 * 4 * 128 * 128 * 2
+    assert lib.glt_attention_fwd(16, 16, 16, 16, 1, 16, 4, 1, 128, 0.125, 1, None, 0, None) == 5  # GLT_ERR_WORKSPACE
     d2 = F.MlpDesc(16, 64, 128, 64, F.DTYPE_BF16, 0, 0, None, None)  # N < I
     assert lib.glt_mlp_fwd(ctypes.byref(d2), ctypes.byref(w), 1, 1, None, None, 1, None) == 2
     d3 = F.MlpDesc(16, 64, 64, 64, 7, 0, 0, None, None)
