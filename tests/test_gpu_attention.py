@@ -17,6 +17,8 @@ pytestmark = pytest.mark.gpu
     (1, 300, 4, 2, False),    # non-causal
     (1, 1, 4, 1, True),       # a single token
     (1, 520, 32, 8, True),    # the decoder layer's head layout, several key tiles per block
+    (3, 1000, 8, 2, True),    # four 256-query blocks (the last ragged), last key tile 40 keys
+    (1, 700, 4, 4, False),    # non-causal, no head grouping, ragged last tile
 ])
 def test_attention_vs_oracle(dev, B, T, Hq, Hkv, causal):
     """bf16 budget with q = 3 roundings: probabilities, output, inputs."""
@@ -77,3 +79,30 @@ def test_attention_full_decoder_layer_shape(dev):
                 p = np.exp(s - s.max())
                 ref[b, i, h] = (p / p.sum()) @ vn[b, :t + 1, g]
     assert_bf16_budget(got, ref, q=3, what="attention at the decoder-layer shape")
+
+
+def test_attention_workspace_reused_across_calls(dev):
+    """The transposed copy of v in the workspace is rewritten by every call:
+    two calls with different v (and a shorter T the second time) through the
+    C-ABI into one workspace each match the oracle."""
+    import ctypes
+    import torch
+    from glt_amd import _ffi as F
+    bf = torch.bfloat16
+    B, Hq, Hkv, hd = 2, 8, 2, 128
+    lib = F.load()
+    nb = lib.glt_attention_workspace_size(B, 300, Hkv, hd)
+    ws = torch.full((nb,), 0x7F, dtype=torch.uint8, device="cuda")  # non-zero junk first
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    for T, seed in ((300, 21), (130, 22)):
+        assert lib.glt_attention_workspace_size(B, T, Hkv, hd) <= nb
+        q = draw((B, T, Hq, hd), seed, 1)
+        k = draw((B, T, Hkv, hd), seed, 2)
+        v = draw((B, T, Hkv, hd), seed, 3)
+        qd, kd, vd = to_dev(q, bf), to_dev(k, bf), to_dev(v, bf)
+        out = torch.empty_like(qd)
+        print(f"case B={B} T={T}", flush=True)
+        F.call("glt_attention_fwd", p(qd), p(kd), p(vd), p(out), B, T, Hq, Hkv, hd, hd ** -0.5, 1, p(ws), nb, sp)
+        torch.cuda.synchronize()
+        assert_bf16_budget(to_np(out), O.attention(q, k, v, causal=True), q=3, what=f"attention T={T} (reused workspace)")
