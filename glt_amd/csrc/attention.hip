@@ -37,7 +37,6 @@
 // arithmetic phase m, group B V^T(m+1) in its, each waits for its loads at
 // the end of its next MFMA phase.
 #include <atomic>
-#include <type_traits>
 
 #include "common.hpp"
 
@@ -97,13 +96,6 @@ __device__ __forceinline__ void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-}
-// A copy of x the compiler cannot see through: address arithmetic based on
-// it is redone where it is used instead of being hoisted out of the loop
-// and kept live in registers (or spilled) across the MFMA phases.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
 }
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
@@ -192,8 +184,10 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
   const __amdgpu_buffer_rsrc_t rv = uni_rsrc_a(vt, kExtentA);
   const uint32_t row_bytes = (uint32_t)(kv_ld * 2);
   const uint32_t kv_base = (uint32_t)(((int64_t)b * T * kv_ld + (int64_t)g * kHd) * 2);
-  // ---- K tile (group B): 16 direct-to-LDS loads of 1 KB, four per
-  // wavefront; load i of wavefront w fills rows 4(4i+w) .. +3, lane L takes
+  // ---- K tile (by one group of four wavefronts: group A in its
+  // arithmetic phases, K(1) by group B in the prologue): 16 direct-to-LDS
+  // loads of 1 KB, four per wavefront; load i of the group's wavefront w
+  // fills rows 4(4i+w) .. +3, lane L takes
   // row +L/16 and physical chunk L&15 = logical chunk ^ (row & 15). The
   // per-lane part of each load's offset is fixed; the tile's part rides in
   // the scalar offset (tiles wholly below T) or is added with the key bound
@@ -263,36 +257,33 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
   for (int i = 0; i < 4; ++i) pb[i] = bf16x8{};
   float m_run = kMaskVal, l_run = 0.f;
 
-  // MFMA phase m: S^T(m) = K(m) . Q^T (K slot m&1) and O^T += V^T(m-1) .
+  // MFMA phase m: S^T(m) = K(m) . Q^T (K slot m % 3) and O^T += V^T(m-1) .
   // P^T(m-1) (V^T slot (m-1)&1), the two products' MFMAs interleaved.
-  auto mfma_phase = [&](int m, auto do_s, auto do_pv) {
-    constexpr bool S = decltype(do_s)::value, PV = decltype(do_pv)::value;
+  auto mfma_phase = [&](int m) {
     const char* kt = smem + (m % 3) * kTileBytes;
     const char* vt = smem + kVtBase + ((m + 1) & 1) * kTileBytes;
-    if constexpr (S) {
-      sacc[0] = f32x16{};
-      sacc[1] = f32x16{};
-    }
-    // MFMA i: S^T step (key block i & 1, d step i >> 1) and PV step (16-key
-    // step i >> 2, d block i & 3); each fragment is read two MFMA pairs
-    // ahead (a fence per pair keeps the reads from all being hoisted).
+    sacc[0] = f32x16{};
+    sacc[1] = f32x16{};
+    // MFMA pair i: S^T step (key block i & 1, d step i >> 1) and PV step
+    // (16-key step i >> 2, d block i & 3); each fragment is read three
+    // pairs ahead (a fence per pair keeps the reads from all being hoisted).
     auto kread = [&](int i) { return *reinterpret_cast<const bf16x8*>(kt + (i & 1) * 8192 + kfa[i >> 1]); };
     auto vread = [&](int i) { return *reinterpret_cast<const bf16x8*>(vt + (i & 3) * 4096 + vfa[i >> 2]); };
     bf16x8 kq[3], vq[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      if constexpr (S) kq[i] = kread(i);
-      if constexpr (PV) vq[i] = vread(i);
+      kq[i] = kread(i);
+      vq[i] = vread(i);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const bf16x8 kf = kq[i % 3], vf = vq[i % 3];
       if (i + 3 < 16) {
-        if constexpr (S) kq[i % 3] = kread(i + 3);
-        if constexpr (PV) vq[i % 3] = vread(i + 3);
+        kq[i % 3] = kread(i + 3);
+        vq[i % 3] = vread(i + 3);
       }
-      if constexpr (S) sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[i >> 1], sacc[i & 1], 0, 0, 0);
-      if constexpr (PV) o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[i >> 2], o[i & 3], 0, 0, 0);
+      sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[i >> 1], sacc[i & 1], 0, 0, 0);
+      o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[i >> 2], o[i & 3], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -370,7 +361,6 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
       pb[s2] = __builtin_bit_cast(bf16x8, u32x4{s0[0], s1[0], s0[1], s1[1]});
     }
   };
-  using YES = std::true_type;
   // MFMA phase m of this wavefront. Every MFMA phase runs both products:
   // phase 0's PV step multiplies the zeroed P^T operands with the zeroed
   // V^T slot 1 (adds exactly 0), and phase ntiles' S^T is computed and never
@@ -378,7 +368,7 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
   // phase before (the next barrier publishes them).
   auto m_phase = [&](int m) {
     __builtin_amdgcn_s_setprio(1);
-    mfma_phase(m, YES{}, YES{});
+    mfma_phase(m);
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
   };
