@@ -19,6 +19,7 @@ pytestmark = pytest.mark.gpu
     (1, 520, 32, 8, True),    # the decoder layer's head layout, several key tiles per block
     (3, 1000, 8, 2, True),    # four 256-query blocks (the last ragged), last key tile 40 keys
     (1, 700, 4, 4, False),    # non-causal, no head grouping, ragged last tile
+    (2, 150, 6, 2, True),     # three query heads per kv head
 ])
 def test_attention_vs_oracle(dev, B, T, Hq, Hkv, causal):
     """bf16 budget with q = 3 roundings: probabilities, output, inputs."""
