@@ -69,9 +69,13 @@ constexpr bf16x2_t kOnes2 = {(__bf16)1.0f, (__bf16)1.0f};
 // and r1 = [a of lanes 32-63 | b of lanes 32-63] (lanes 0-31 | 32-63).
 // For a value held per lane, r0/r1 of swap(x, x) are the values of the two
 // lanes of the pair (l, l^32), in every lane.
+// Maxima use the NaN-propagating maximum (v_maximum3_f32): fmaxf would make
+// the compiler canonicalise each MFMA result first (one more instruction per
+// score pair); no score is NaN.
+__device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float pair_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return fmax_nc(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -305,18 +309,17 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
         for (int e = 0; e < 16; ++e)
           sacc[kb][e] = (32 * kb + 8 * (e >> 2) + (e & 3)) < lim ? sacc[kb][e] : kMaskVal;
     }
-    // four independent chains (a tree's latency, not 32 dependent steps)
-    float m4[4];
+    // two independent chains of three-input maxima, one per key block
+    float m2[2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      m4[c] = fmaxf(sacc[c >> 1][8 * (c & 1)], sacc[c >> 1][8 * (c & 1) + 1]);
+    for (int kb = 0; kb < 2; ++kb) {
+      m2[kb] = sacc[kb][0];
 #pragma unroll
-      for (int e = 2; e < 8; ++e) m4[c] = fmaxf(m4[c], sacc[c >> 1][8 * (c & 1) + e]);
+      for (int e = 1; e < 16; ++e) m2[kb] = fmax_nc(m2[kb], sacc[kb][e]);
     }
-    float mt = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
-    mt = pair_max(mt) * scale_log2;
+    float mt = pair_max(fmax_nc(m2[0], m2[1])) * scale_log2;
     if (__any(mt > m_run + kSlack)) {
-      const float m_new = fmaxf(m_run, mt);
+      const float m_new = fmax_nc(m_run, mt);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
@@ -336,17 +339,18 @@ attn_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, 
         pk[kb][gi][1] = pack2_rne(p4[2], p4[3]);
       }
     // row sum of the rounded probabilities the PV product uses: a dot
-    // product with (1, 1) per packed pair, four independent chains
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    // product with (1, 1) per packed pair, two independent chains, the
+    // first continuing the running sum
+    float ps[2] = {l_run, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi)
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
-          ps[2 * kb + h2] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk[kb][gi][h2]), kOnes2,
-                                                             ps[2 * kb + h2], false);
-    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+          ps[h2] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk[kb][gi][h2]), kOnes2, ps[h2],
+                                                   false);
+    l_run = ps[0] + ps[1];
     // 16-key step s2 covers keys 16 s2 .. +15 = groups 2(s2&1), 2(s2&1)+1
     // of key block s2>>1. The lane with lh = 0 needs keys +0..7 (its own
     // first four, its partner's next four), lh = 1 keys +8..15: swap(own
