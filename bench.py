@@ -315,6 +315,9 @@ def main():
                    "tokens": M, "hidden": D, "base_intermediate": I, "graft_slice": S, "parallelism": "none (1 GPU)"},
         "step_mfma_frac": round(STEP_FLOP / (ms_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "gemm_mfma_frac": round(STEP_FLOP / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        # the fwd+bwd GEMM path alone (sum of the step's GEMM launches), beside
+        # the full step of "value"
+        "gemm_path": {"ms": round(gemm_ms, 4), "tokens_per_s": round(M / (gemm_ms * 1e-3), 1)},
         "roofline": roofline,
         "hbm_kernels": hbm,
         "cpu_baseline": cpu,
