@@ -209,6 +209,38 @@ def main():
             v["tflops"] = GEMM_FLOP[k] / (v["ms_per_step"] * 1e-3) / 1e12
             v["mfma_frac"] = v["tflops"] / PEAK_BF16_TFLOPS
     gemm_ms = sum(kernels[k]["ms_per_step"] for k in GEMM_FLOP if k in kernels)
+
+    # One GPU's share of an 8-way token-parallel step: the same step on the
+    # first M / 8 tokens of the same buffers (rows are contiguous), with the
+    # same graft weights and optimizer state. The multi-GPU step would add
+    # the all-reduce of the graft gradients, which is not run here.
+    m_share = M // 8
+    desc_share = F.MlpDesc(m_share, D, I, N, F.DTYPE_BF16, F.MLP_EXPLICIT | F.MLP_DY_F32, 1, sl, None)
+    assert lib.glt_mlp_bwd_workspace_size(ctypes.byref(desc_share)) <= ws_bytes
+
+    def step_share(i):
+        F.call("glt_rmsnorm_fwd", p(x_raw), p(gamma), p(x), p(var), m_share, D, EPS, sp)
+        F.call("glt_mlp_fwd", ctypes.byref(desc_share), ctypes.byref(base), p(x), p(y), p(g), p(u), p(inter), sp)
+        F.call("glt_mlp_rmsnorm_bwd", ctypes.byref(desc_share), ctypes.byref(base), p(x), p(dy), p(g), p(u),
+               p(inter), p(dx), gg, p(ws), ws_bytes, p(x_raw), p(gamma), p(var), EPS, p(dx_raw), sp)
+        F.call("glt_adamw_graft_step", sl, 1, gptr, mptr, vptr, pkptr, 7, i, LR, B1, B2, AEPS, WD, CLIP, p(clip_ws),
+               clip_ws_bytes, sp)
+
+    for i in range(args.warmup):
+        step_share(i)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step_share(args.warmup + i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_share = ev0.elapsed_time(ev1) / args.steps
+    share = {"tokens": m_share, "ms_per_step": round(ms_share, 4),
+             "tokens_per_s": round(m_share / (ms_share * 1e-3), 1),
+             "mfma_frac": round(STEP_FLOP / 8 / (ms_share * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+             "note": "one GPU's share of an 8-way token-parallel step of the same workload; the gradient "
+                     "all-reduce of the multi-GPU step is not run"}
+    log(f"[bench] 1/8 share ({m_share} tokens): {ms_share:.3f} ms/step")
     dom = max((k for k in kernels if k in GEMM_FLOP), key=lambda k: kernels[k]["ms_per_step"])
     dom_flop = GEMM_FLOP[dom] / kernels[dom]["launches_per_step"]  # per launch
     achieved = dom_flop / (kernels[dom]["avg_ms"] * 1e-3) / 1e12
@@ -318,6 +350,7 @@ def main():
         # the fwd+bwd GEMM path alone (sum of the step's GEMM launches), beside
         # the full step of "value"
         "gemm_path": {"ms": round(gemm_ms, 4), "tokens_per_s": round(M / (gemm_ms * 1e-3), 1)},
+        "dp8_share": share,
         "roofline": roofline,
         "hbm_kernels": hbm,
         "cpu_baseline": cpu,
